@@ -1,0 +1,127 @@
+/*
+ * gqa_decode.h -- C ABI of the MI355X (gfx950) GQA paged-decode kernels.
+ *
+ * Single-token GQA decode attention over a paged bf16 KV cache, head dim 128:
+ *
+ *   out[b, h, :] = softmax_t( scale * <q[b, h, :], K_b[t, kv(h), :]> ) . V_b[t, kv(h), :]
+ *   kv(h)        = h / (Hq / Hkv)                       (consecutive grouping)
+ *   K_b[t]       = k_cache[block_table[b, t / block_size], t % block_size]
+ *
+ * Tensor layouts (all row-major, contiguous, device memory):
+ *   q            [B, Hq, 128]                       bf16 (raw bits, uint16_t)
+ *   k_cache      [num_blocks, block_size, Hkv, 128] bf16 (NHD)
+ *   v_cache      [num_blocks, block_size, Hkv, 128] bf16 (NHD)
+ *   block_table  [B, max_blocks]                    int32; entries at or beyond
+ *                                                    ceil(seq_lens[b]/block_size)
+ *                                                    are never read
+ *   seq_lens     [B]                                int32, each >= 1
+ *   out          [B, Hq, 128]                       bf16, round-to-nearest-even
+ *
+ * Every launcher is asynchronous on `stream`, allocates nothing, and returns
+ * hipSuccess (0) or a hipError_t code: hipErrorInvalidValue (1) for arguments
+ * it rejects before launching, otherwise the error hipGetLastError() reports
+ * after the launch. seq_lens[b] == 0 is unsupported (the result is NaN, as in
+ * the reference). All entry points are reentrant; results are bitwise
+ * deterministic for identical inputs.
+ *
+ * Reference counterparts (paths relative to the reference checkout):
+ *   gqa_decode_v0_launch   include/gqa_decode.h:6-10,  kernels/gqa_decode/v0_naive.cu:27-36
+ *   gqa_decode_v1_launch   include/gqa_decode.h:12-16, kernels/gqa_decode/v1_vectorized.cu:73-82
+ *   gqa_decode_v2_launch   include/gqa_decode.h:18-23, kernels/gqa_decode/v2_splitkv.cu:110-125
+ * The names and argument order are the reference's; the differences are the
+ * C linkage, HIP stream type, bf16 passed as raw uint16_t bits, and the
+ * int error code in place of void.
+ */
+#ifndef GQA_DECODE_H_
+#define GQA_DECODE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Entry points are the only symbols the library exports. */
+#define GQA_DECODE_API __attribute__((visibility("default")))
+
+/* Head dimension the kernels are built for. */
+#define GQA_DECODE_HEAD_DIM 128
+/* Largest num_splits gqa_decode_v2_launch accepts (python/gqa_decode_ext.cpp:102-103). */
+#define GQA_DECODE_MAX_SPLITS 512
+
+/* v0: correctness-first kernel, one wave64 per (b, q-head), token-serial online
+ * softmax. Replaces gqa_decode_v0_launch (include/gqa_decode.h:6-10). */
+GQA_DECODE_API int gqa_decode_v0_launch(const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const int* block_table,
+                         const int* seq_lens, uint16_t* out, int B, int Hq,
+                         int Hkv, int block_size, int max_blocks, float scale,
+                         hipStream_t stream);
+
+/* v1: single-pass scan, one workgroup per (b, kv-head) holding the whole
+ * q-head group, 16-byte row loads, fp32 online-softmax state.
+ * Replaces gqa_decode_v1_launch (include/gqa_decode.h:12-16). */
+GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const int* block_table,
+                         const int* seq_lens, uint16_t* out, int B, int Hq,
+                         int Hkv, int block_size, int max_blocks, float scale,
+                         hipStream_t stream);
+
+/* v2: split-KV. A partial kernel writes one unnormalised fp32 (m, l, acc) state
+ * per (b, q-head, split) to the caller's workspace, then a log-sum-exp merge
+ * kernel writes `out`. Workspace layout (the reference's, v2_splitkv.cu:10-12):
+ *   ws_acc [B, Hq, num_splits, 128] fp32, ws_m / ws_l [B, Hq, num_splits] fp32
+ * ws_m holds the segment's max of scale*<q,k> (natural-log units), ws_l the sum
+ * of exp(score - ws_m), ws_acc the exp-weighted sum of V rows. An empty segment
+ * stores (-inf, 0, 0). num_splits must be in [1, GQA_DECODE_MAX_SPLITS];
+ * num_splits == 1 gives output bitwise equal to gqa_decode_v1_launch.
+ * Replaces gqa_decode_v2_launch (include/gqa_decode.h:18-23). */
+GQA_DECODE_API int gqa_decode_v2_launch(const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const int* block_table,
+                         const int* seq_lens, uint16_t* out, int B, int Hq,
+                         int Hkv, int block_size, int max_blocks, float scale,
+                         int num_splits, float* ws_acc, float* ws_m,
+                         float* ws_l, hipStream_t stream);
+
+/* The two halves of gqa_decode_v2_launch, for callers that produce or combine
+ * split states themselves (e.g. a context-parallel decode that all-gathers
+ * partial states across devices and then merges them). Same arguments and
+ * workspace contract as gqa_decode_v2_launch; _partial writes only the
+ * workspace, _merge reads only the workspace. Reference counterparts: the
+ * partial and merge launches inside gqa_decode_v2_launch
+ * (kernels/gqa_decode/v2_splitkv.cu:115-124). */
+GQA_DECODE_API int gqa_decode_v2_partial_launch(const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, const int* block_table,
+                                 const int* seq_lens, int B, int Hq, int Hkv,
+                                 int block_size, int max_blocks, float scale,
+                                 int num_splits, float* ws_acc, float* ws_m,
+                                 float* ws_l, hipStream_t stream);
+
+GQA_DECODE_API int gqa_decode_v2_merge_launch(const float* ws_acc, const float* ws_m,
+                               const float* ws_l, uint16_t* out, int B, int Hq,
+                               int num_splits, hipStream_t stream);
+
+/* Bytes of workspace gqa_decode_v2_launch needs for (B, Hq, num_splits), all
+ * three arrays together: B*Hq*num_splits*(128 + 2)*4. Returns 0 for
+ * non-positive arguments. No reference counterpart (the reference sizes the
+ * workspace inline at python/gqa_decode_ext.cpp:106-109). */
+GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits);
+
+/* Split count that fills the device: enough (b, kv-head, split) workgroups
+ * for every CU, while keeping each split long enough that the workspace
+ * round trip stays small next to the KV stream. max_blocks*block_size is
+ * taken as the longest sequence. num_cus <= 0 means "query the current
+ * device". Returns a value in [1, GQA_DECODE_MAX_SPLITS], or 0 for invalid
+ * arguments. No reference counterpart: the reference defaults to 8
+ * (python/gqa_decode_ext.cpp:133) and picks the best value by sweep
+ * (bench/run_matrix.py:84-94). Pure host code. */
+GQA_DECODE_API int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size,
+                               int max_blocks, int num_cus);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GQA_DECODE_H_ */

@@ -1,0 +1,166 @@
+"""Synthetic paged-decode inputs and the speed-of-light arithmetic.
+
+Counterpart of the reference's bench/common.py:16-72 and of the case builder
+in tests/test_gqa_decode.py:27-69: seeded q/k/v, a shuffled physical block
+pool, -1 padding past each request's blocks, and optional NaN poisoning of
+every slot a kernel must not read (unallocated blocks and the tail slots of
+each request's last block).
+"""
+
+import math
+
+import numpy as np
+import torch
+
+D = 128
+HBM_PEAK_BYTES_PER_S = 8.0e12  # MI355X HBM3E, AMD spec
+
+# BASELINE.json configs 1..5.
+CONFIGS = {
+    "c1": dict(Hq=32, Hkv=8, B=1, S=512, bs=16, pool=64,
+               desc="plumbing: B=1 S=512 block=16, 64-block pool (32 used)"),
+    "c2": dict(Hq=32, Hkv=8, B=32, S=8192, bs=16, pool=16384,
+               desc="representative: 32Q/8KV B=32 S=8192 block=16 (1 GiB KV)"),
+    "c3": dict(Hq=32, Hkv=8, B=8, S=32768, bs=64, pool=4096,
+               desc="long context: 32Q/8KV B=8 S=32768 block=64 (1 GiB KV)"),
+    "c4": dict(Hq=64, Hkv=8, B=32, S=32768, bs=64, pool=16384,
+               desc="wide GQA: 64Q/8KV B=32 S=32768 block=64 (4 GiB KV)"),
+    "c5": dict(Hq=32, Hkv=8, B=128, S=None, S_max=32768, bs=16, pool_factor=1.25,
+               desc="ragged: 32Q/8KV B=128 S~U[1,32768] block=16, pool 1.25x"),
+}
+
+
+def config_seq_lens(name, seed=0):
+    """Per-request lengths of a config (the ragged one draws from a seeded CPU
+    generator, so the lengths are identical on every machine)."""
+    cfg = CONFIGS[name]
+    if cfg["S"] is not None:
+        return [cfg["S"]] * cfg["B"]
+    g = torch.Generator().manual_seed(seed + 1)
+    return torch.randint(1, cfg["S_max"] + 1, (cfg["B"],), generator=g).tolist()
+
+
+def make_case(S_list, Hq, Hkv, bs, *, pool=None, pool_factor=None, seed=0, device="cuda",
+              qkv_std=1.0, poison=False, max_blocks=None):
+    """Build (q, k_cache, v_cache, block_table, seq_lens) on `device`.
+
+    q/k/v ~ qkv_std * N(0, 1) in bf16 from a seeded generator on `device`.
+    The physical pool holds `pool` blocks (default ceil(pool_factor * needed),
+    or exactly the needed count); block ids come from a seeded CPU permutation
+    of the pool, request b taking the next ceil(S_b / bs) ids. Entries past a
+    request's blocks are -1. With poison=True every unallocated block and every
+    slot past S_b in a request's last block is NaN.
+    """
+    B = len(S_list)
+    n_blocks = [(int(s) + bs - 1) // bs for s in S_list]
+    needed = sum(n_blocks)
+    if pool is None:
+        pool = math.ceil(needed * pool_factor) if pool_factor else needed
+    if pool < needed:
+        raise ValueError(f"pool of {pool} blocks < {needed} needed")
+    if max_blocks is None:
+        max_blocks = max(n_blocks) if n_blocks else 1
+
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(B, Hq, D, device=device, generator=gen, dtype=torch.float32)
+    q = (q * qkv_std).to(torch.bfloat16)
+    k_cache = torch.empty(pool, bs, Hkv, D, device=device, dtype=torch.bfloat16)
+    v_cache = torch.empty_like(k_cache)
+    # Fill in slabs of blocks to bound the fp32 temporary.
+    slab = max(1, (64 << 20) // (bs * Hkv * D))
+    for cache in (k_cache, v_cache):
+        for i in range(0, pool, slab):
+            n = min(slab, pool - i)
+            x = torch.randn(n, bs, Hkv, D, device=device, generator=gen, dtype=torch.float32)
+            cache[i:i + n] = (x * qkv_std).to(torch.bfloat16)
+
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))
+    block_table = torch.full((B, max_blocks), -1, dtype=torch.int32)
+    used = torch.zeros(pool, dtype=torch.bool)
+    off = 0
+    for b in range(B):
+        ids = perm[off:off + n_blocks[b]]
+        block_table[b, :n_blocks[b]] = ids.to(torch.int32)
+        used[ids] = True
+        off += n_blocks[b]
+
+    if poison:
+        unused = (~used).nonzero().flatten().to(device)
+        if unused.numel():
+            k_cache.index_fill_(0, unused, float("nan"))
+            v_cache.index_fill_(0, unused, float("nan"))
+        for b in range(B):
+            rem = int(S_list[b]) % bs
+            if rem:
+                last = int(block_table[b, n_blocks[b] - 1])
+                k_cache[last, rem:] = float("nan")
+                v_cache[last, rem:] = float("nan")
+
+    seq_lens = torch.tensor([int(s) for s in S_list], dtype=torch.int32, device=device)
+    return q, k_cache, v_cache, block_table.to(device), seq_lens
+
+
+def make_config_case(name, seed=0, device="cuda", poison=False):
+    cfg = CONFIGS[name]
+    S_list = config_seq_lens(name, seed)
+    return make_case(S_list, cfg["Hq"], cfg["Hkv"], cfg["bs"], pool=cfg.get("pool"),
+                     pool_factor=cfg.get("pool_factor"), seed=seed, device=device,
+                     poison=poison)
+
+
+def kv_bytes(S_list, Hkv):
+    """Algorithmic K+V bytes of one decode step: sum_b S_b * Hkv * 128 * 2 * 2
+    (bench/common.py:67-69 of the reference, per request)."""
+    return sum(int(s) for s in S_list) * Hkv * D * 2 * 2
+
+
+def sol_us(nbytes, peak=HBM_PEAK_BYTES_PER_S):
+    """Speed-of-light time of streaming nbytes from HBM once, in microseconds."""
+    return nbytes / peak * 1e6
+
+
+def time_op(fn, warmup=10, runs=50):
+    """Median time of fn() in milliseconds, HIP events on the current stream
+    around each call (bench/common.py:49-64 of the reference)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(runs):
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def bits(t):
+    """bf16 device tensor -> uint16 numpy array of raw bits (on the host)."""
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_case(case, batches=None):
+    """Host (numpy) copy of (q, k, v, block_table, seq_lens). With `batches`,
+    only those requests are kept and their blocks are compacted into a small
+    pool with remapped ids, so a large case can be checked on a subset."""
+    q, k, v, bt, sl = case
+    if batches is None:
+        return bits(q), bits(k), bits(v), bt.cpu().numpy(), sl.cpu().numpy()
+    batches = list(batches)
+    bs = k.shape[1]
+    sl_h = sl.cpu().numpy()[batches]
+    bt_h = bt.cpu().numpy()[batches]
+    n = [(int(s) + bs - 1) // bs for s in sl_h]
+    ids = np.concatenate([bt_h[i, :n[i]] for i in range(len(batches))]).astype(np.int64)
+    idx = torch.from_numpy(ids).to(k.device)
+    new_bt = np.full((len(batches), max(n)), -1, dtype=np.int32)
+    off = 0
+    for i in range(len(batches)):
+        new_bt[i, :n[i]] = np.arange(off, off + n[i])
+        off += n[i]
+    return (bits(q[batches]), bits(k.index_select(0, idx)), bits(v.index_select(0, idx)),
+            new_bt, sl_h.astype(np.int32))

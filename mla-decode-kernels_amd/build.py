@@ -1,0 +1,111 @@
+"""Build recipe for the gfx950 GQA decode library and its PyTorch extension.
+
+    python mla-decode-kernels_amd/build.py            # kernels + extension
+    python mla-decode-kernels_amd/build.py --no-ext   # kernel library only
+
+Products (in-tree, git-ignored, shipped with the source tree):
+  lib/libgqa_decode_hip.so   hipcc --offload-arch=gfx950: every kernel + the C ABI
+  lib/gqa_decode_ext*.so     g++: host-only torch operator layer linking the above
+
+The extension is compiled as plain C++ (no .cu/.hip source, so torch's
+hipify pass never runs); it reaches the GPU only through the C ABI.
+"""
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+import time
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_ROOT = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+INCLUDE = os.path.join(REPO_ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+KERNEL_LIB = os.path.join(LIB_DIR, "libgqa_decode_hip.so")
+HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip"]
+# Packed fp32 VALU ops are disabled for all device code.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd, cwd=None):
+    t0 = time.time()
+    proc = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass does not know the device-only feature flag; drop that note.
+    out = "\n".join(
+        ln for ln in proc.stdout.splitlines()
+        if "packed-fp32-ops' is not a recognized feature" not in ln
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+    return time.time() - t0
+
+
+def build_kernels():
+    os.makedirs(LIB_DIR, exist_ok=True)
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    tmp = KERNEL_LIB + ".tmp"
+    dt = _run([hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    os.replace(tmp, KERNEL_LIB)
+    print(f"built {os.path.relpath(KERNEL_LIB, REPO_ROOT)} in {dt:.1f}s")
+    return KERNEL_LIB
+
+
+def ext_filename():
+    return "gqa_decode_ext" + sysconfig.get_config_var("EXT_SUFFIX")
+
+
+def build_extension():
+    import torch
+    from torch.utils import cpp_extension
+
+    if not os.path.exists(KERNEL_LIB):
+        raise RuntimeError("kernel library missing; build it first")
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = cpp_extension.include_paths() + [INCLUDE, os.path.join(ROCM, "include"),
+                                            sysconfig.get_paths()["include"]]
+    out = os.path.join(LIB_DIR, ext_filename())
+    tmp = out + ".tmp"
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-DTORCH_EXTENSION_NAME=gqa_decode_ext", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *[f"-I{i}" for i in incs],
+        os.path.join(PKG_DIR, "python", "gqa_decode_ext.cpp"),
+        "-o", tmp,
+        f"-L{LIB_DIR}", "-lgqa_decode_hip", "-Wl,-rpath,$ORIGIN",
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        f"-Wl,-rpath,{torch_lib}",
+        f"-L{os.path.join(ROCM, 'lib')}", "-lamdhip64",
+    ]
+    dt = _run(cmd)
+    os.replace(tmp, out)
+    print(f"built {os.path.relpath(out, REPO_ROOT)} in {dt:.1f}s")
+    return out
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--no-ext", action="store_true", help="build the kernel library only")
+    args = ap.parse_args(argv)
+    if shutil.which(os.path.join(ROCM, "bin", "hipcc")) is None:
+        sys.exit(f"hipcc not found under {ROCM}")
+    build_kernels()
+    if not args.no_ext:
+        build_extension()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,440 @@
+// v1 (single pass) and v2 (split-KV partial + log-sum-exp merge) decode
+// kernels for gfx950.
+//
+// Work decomposition. One workgroup of kWaves wave64s owns one
+// (b, kv-head, q-head chunk, split) and serves every q-head of the GQA group
+// from the same K/V registers, so each K/V row crosses HBM once (the
+// reference's per-q-head CTAs rely on L2 for that: kernels/gqa_decode/
+// v2_splitkv.cu:18-24). Tiles of 16 tokens are dealt round-robin to the waves
+// of the workgroup. Inside a wave the 64 lanes form 4 DPP rows of 16 lanes; a
+// row reads one 256-byte K (or V) head row with 16-byte loads, so one load
+// instruction covers 4 tokens and a tile is 4 K loads + 4 V loads per lane.
+//
+// Per tile: QK^T with v_dot2c_f32_bf16 on the packed bf16 q and K words, a
+// 4-step DPP row reduction, then one online-softmax update per (row, head) for
+// the whole tile (max over its 4 tokens, one rescale of l and acc) in base-2
+// units, and PV as fp32 FMAs. The next tile's loads are issued before the
+// current tile is consumed. At the end the 4 row states of a wave and then the
+// kWaves wave states are merged in a fixed order (bitwise deterministic).
+//
+// Split rule: segment `split` of request b covers
+// [split*chunk, min(S, (split+1)*chunk)) with chunk = ceil(S/num_splits)
+// rounded up to a multiple of 16 tokens (v2_splitkv.cu:30-32 without the
+// rounding). The rounding keeps every tile inside one cache block whenever
+// block_size is a multiple of 16, which lets the block id be a scalar load.
+// Splits past the end of a short request are empty and store the neutral
+// state (-inf, 0, 0), whose merge factor is 0 (v2_splitkv.cu:33-40).
+#include "gqa_device.hpp"
+#include "gqa_launch.hpp"
+#include "gqa_decode.h"
+
+namespace gqa {
+
+constexpr int kTile = 16;   // tokens per wave per tile
+constexpr int kLoads = 4;   // 16-byte K loads (and V loads) per lane per tile
+constexpr int kWaves = 4;   // waves per workgroup
+
+struct ScanArgs {
+  const uint16_t* q;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  const int* block_table;
+  const int* seq_lens;
+  uint16_t* out;  // single-pass mode: normalised bf16 output (num_splits == 1)
+  float* ws_acc;  // split mode: unnormalised per-split state
+  float* ws_m;
+  float* ws_l;
+  int Hq, Hkv, G, nchunk, block_size, max_blocks, num_splits;
+  FastDiv bs_div;
+  float scale_log2e;  // scale * log2(e): scores are kept in base-2 units
+};
+
+struct TileRegs {
+  uint4 k[kLoads];
+  uint4 v[kLoads];
+};
+
+template <int GH, bool kBlockUniform>
+__global__ __launch_bounds__(64 * kWaves) void gqa_decode_scan_kernel(const ScanArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 4;  // DPP row: token 4j + r of each load j
+  const int c = lane & 15;  // dims [8c, 8c + 8)
+  const int hkv = blockIdx.x / a.nchunk;
+  const int hc = blockIdx.x - hkv * a.nchunk;
+  const int b = blockIdx.y, split = blockIdx.z;
+  const int h0 = hkv * a.G + hc * GH;  // first q-head of this chunk
+  const int nh = min(GH, a.G - hc * GH);
+
+  const int S = max(a.seq_lens[b], 0);
+  const int ns = a.num_splits;
+  const int chunk = ((S + ns - 1) / ns + (kTile - 1)) & ~(kTile - 1);
+  const int seg_start = min(split * chunk, S);
+  const int seg_end = min(S, seg_start + chunk);
+  const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
+  const int my_tiles = ntiles > wv ? (ntiles - wv + kWaves - 1) / kWaves : 0;
+
+  uint4 qf[GH];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    qf[j] = make_uint4(0, 0, 0, 0);
+    if (j < nh)
+      qf[j] = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * a.Hq + h0 + j) * kHeadDim + 8 * c);
+  }
+
+  float m[GH], l[GH], acc[GH][8];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    m[j] = kNegInf;
+    l[j] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[j][d] = 0.f;
+  }
+
+  const uint32_t row_elems = (uint32_t)a.Hkv * kHeadDim;  // elements between slots
+  const uint16_t* kbase = a.k_cache + (size_t)hkv * kHeadDim + 8 * c;
+  const uint16_t* vbase = a.v_cache + (size_t)hkv * kHeadDim + 8 * c;
+  const int* bt = a.block_table + (size_t)b * a.max_blocks;
+  const int bs = a.block_size;
+
+  auto tile_start = [&](int k) { return seg_start + kTile * (wv + kWaves * k); };
+
+  // Issue the K and V loads of this wave's tile k. Tokens at or past seg_end
+  // read the tile's first token instead (always valid), so no load touches an
+  // unallocated block or a tail slot; their scores are masked in consume().
+  auto issue = [&](int k, TileRegs& t) {
+    const int ts = tile_start(k);
+    if constexpr (kBlockUniform) {
+      // The 16 tokens of the tile share one block: scalar block-id load, a
+      // uniform 64-bit block base and 32-bit per-lane offsets inside it.
+      const uint32_t lb = fastdiv((uint32_t)ts, a.bs_div);
+      const int slot0 = ts - (int)lb * bs;
+      const size_t blk = (size_t)bt[lb] * ((size_t)bs * row_elems) + (size_t)hkv * kHeadDim;
+      const uint16_t* kblk = a.k_cache + blk;
+      const uint16_t* vblk = a.v_cache + blk;
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) {
+        const int tok = ts + 4 * j + r;
+        const uint32_t slot = tok < seg_end ? slot0 + 4 * j + r : slot0;
+        const uint32_t off = slot * row_elems + 8 * c;
+        t.k[j] = *reinterpret_cast<const uint4*>(kblk + off);
+        t.v[j] = *reinterpret_cast<const uint4*>(vblk + off);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) {
+        int tok = ts + 4 * j + r;
+        tok = tok < seg_end ? tok : ts;
+        const uint32_t lb = fastdiv((uint32_t)tok, a.bs_div);
+        const int slot = tok - (int)lb * bs;
+        const size_t off = ((size_t)bt[lb] * bs + slot) * row_elems;
+        t.k[j] = *reinterpret_cast<const uint4*>(kbase + off);
+        t.v[j] = *reinterpret_cast<const uint4*>(vbase + off);
+      }
+    }
+  };
+
+  auto consume = [&](int k, const TileRegs& t) {
+    const int ts = tile_start(k);
+    float s[kLoads][GH];  // scores (base-2 units), then probabilities
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const bool valid = ts + 4 * j + r < seg_end;
+#pragma unroll
+      for (int h = 0; h < GH; ++h) {
+        float d = dot2_bf16(qf[h].x, t.k[j].x, 0.f);
+        d = dot2_bf16(qf[h].y, t.k[j].y, d);
+        d = dot2_bf16(qf[h].z, t.k[j].z, d);
+        d = dot2_bf16(qf[h].w, t.k[j].w, d);
+        d = row16_sum(d);
+        s[j][h] = valid ? d * a.scale_log2e : kNegInf;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
+      const float mn = fmaxf(m[h], mt);
+      const float ms = mn == kNegInf ? 0.f : mn;  // a row with no valid token yet
+      const float al = exp2_fast(m[h] - ms);
+      m[h] = mn;
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) s[j][h] = exp2_fast(s[j][h] - ms);
+      l[h] = fmaf(l[h], al, (s[0][h] + s[1][h]) + (s[2][h] + s[3][h]));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[h][d] *= al;
+    }
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const float vf[8] = {bf16_lo(t.v[j].x), bf16_hi(t.v[j].x), bf16_lo(t.v[j].y),
+                           bf16_hi(t.v[j].y), bf16_lo(t.v[j].z), bf16_hi(t.v[j].z),
+                           bf16_lo(t.v[j].w), bf16_hi(t.v[j].w)};
+#pragma unroll
+      for (int h = 0; h < GH; ++h)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[h][d] = fmaf(s[j][h], vf[d], acc[h][d]);
+    }
+  };
+
+  // Two register tiles in flight: the loop body issues tile k+1 (k+2) before
+  // consuming tile k (k+1) and has no branch, so the wait before each consume
+  // covers only the tile being consumed.
+  if (my_tiles > 0) {
+    TileRegs t0, t1;
+    issue(0, t0);
+    int k = 0;
+    for (; k + 2 < my_tiles; k += 2) {
+      issue(k + 1, t1);
+      consume(k, t0);
+      issue(k + 2, t0);
+      consume(k + 1, t1);
+    }
+    if (k + 1 < my_tiles) {
+      issue(k + 1, t1);
+      consume(k, t0);
+      consume(k + 1, t1);
+    } else {
+      consume(k, t0);
+    }
+  }
+
+  // Merge the 4 row states of the wave (every row ends with the same totals).
+  __shared__ float lds_m[kWaves][GH];
+  __shared__ float lds_l[kWaves][GH];
+  __shared__ float lds_acc[kWaves][GH][kHeadDim];
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+    const float mr = m[h];
+    float M = fmaxf(mr, __shfl_xor(mr, 16, 64));
+    M = fmaxf(M, __shfl_xor(M, 32, 64));
+    const float f = mr == M ? 1.f : exp2_fast(mr - (M == kNegInf ? 0.f : M));
+    float lr = l[h] * f;
+    lr += __shfl_xor(lr, 16, 64);
+    lr += __shfl_xor(lr, 32, 64);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      float x = acc[h][d] * f;
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      acc[h][d] = x;
+    }
+    if (r == 0) {
+      float4* dst = reinterpret_cast<float4*>(&lds_acc[wv][h][8 * c]);
+      dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    }
+    if (lane == 0) {
+      lds_m[wv][h] = M;
+      lds_l[wv][h] = lr;
+    }
+  }
+  __syncthreads();
+
+  // Merge the wave states in wave order and write the result.
+  for (int idx = threadIdx.x; idx < GH * kHeadDim; idx += 64 * kWaves) {
+    const int h = idx / kHeadDim, d = idx % kHeadDim;
+    if (h >= nh) continue;
+    float M = lds_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds_m[w][h]);
+    const float Ms = M == kNegInf ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = lds_m[w][h];
+      const float f = mw == M ? 1.f : exp2_fast(mw - Ms);
+      if (w == 0) {
+        L = lds_l[0][h] * f;
+        A = lds_acc[0][h][d] * f;
+      } else {
+        L = fmaf(lds_l[w][h], f, L);
+        A = fmaf(lds_acc[w][h][d], f, A);
+      }
+    }
+    const size_t bh = (size_t)b * a.Hq + h0 + h;
+    if (a.out) {
+      a.out[bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(finalize(A, L));
+    } else {
+      const size_t st = bh * ns + split;
+      a.ws_acc[st * kHeadDim + d] = A;
+      if (d == 0) {
+        a.ws_m[st] = M * kLn2;  // back to natural-log units
+        a.ws_l[st] = L;
+      }
+    }
+  }
+}
+
+// Log-sum-exp merge of the num_splits states of each (b, q-head) in split order
+// (v2_splitkv.cu:92-108): one wave per (b, q-head), lane i owns dims 2i, 2i+1.
+__global__ __launch_bounds__(256) void gqa_decode_merge_kernel(const float* __restrict__ ws_acc,
+                                                               const float* __restrict__ ws_m,
+                                                               const float* __restrict__ ws_l,
+                                                               uint16_t* __restrict__ out, int BH,
+                                                               int ns) {
+  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (bh >= BH) return;
+  const size_t st0 = (size_t)bh * ns;
+  float M = kNegInf;
+  for (int i = 0; i < ns; ++i) M = fmaxf(M, ws_m[st0 + i]);
+  float L = 0.f, A0 = 0.f, A1 = 0.f;
+  for (int i = 0; i < ns; ++i) {
+    const float mi = ws_m[st0 + i];
+    // Exactly 1 for the split holding the max, so one split is a no-op merge.
+    const float f = mi == M ? 1.f : exp2_fast((mi - M) * kLog2e);
+    const float2 av = reinterpret_cast<const float2*>(ws_acc + (st0 + i) * kHeadDim)[lane];
+    if (i == 0) {
+      L = ws_l[st0] * f;
+      A0 = av.x * f;
+      A1 = av.y * f;
+    } else {
+      L = fmaf(ws_l[st0 + i], f, L);
+      A0 = fmaf(av.x, f, A0);
+      A1 = fmaf(av.y, f, A1);
+    }
+  }
+  const uint32_t lo = f32_to_bf16_bits(finalize(A0, L));
+  const uint32_t hi = f32_to_bf16_bits(finalize(A1, L));
+  reinterpret_cast<uint32_t*>(out + (size_t)bh * kHeadDim)[lane] = lo | (hi << 16);
+}
+
+// q-heads served per workgroup: the whole group up to 8, rounded up to a power
+// of two (extra heads carry q = 0 and are not written); larger groups are cut
+// into chunks of 8 that each scan the same K/V.
+inline int heads_per_wg(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+
+template <int GH>
+hipError_t launch_scan_gh(const ScanArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.block_size % kTile == 0)
+    hipLaunchKernelGGL((gqa_decode_scan_kernel<GH, true>), grid, dim3(64 * kWaves), 0, stream, a);
+  else
+    hipLaunchKernelGGL((gqa_decode_scan_kernel<GH, false>), grid, dim3(64 * kWaves), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                       const int* block_table, const int* seq_lens, uint16_t* out, float* ws_acc,
+                       float* ws_m, float* ws_l, int B, int Hq, int Hkv, int block_size,
+                       int max_blocks, float scale, int num_splits, hipStream_t stream) {
+  ScanArgs a;
+  a.q = q;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.block_table = block_table;
+  a.seq_lens = seq_lens;
+  a.out = out;
+  a.ws_acc = ws_acc;
+  a.ws_m = ws_m;
+  a.ws_l = ws_l;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  const int GH = heads_per_wg(a.G);
+  a.nchunk = (a.G + GH - 1) / GH;
+  a.block_size = block_size;
+  a.max_blocks = max_blocks;
+  a.num_splits = num_splits;
+  a.bs_div = make_fastdiv((uint32_t)block_size);
+  a.scale_log2e = (float)((double)scale * 1.4426950408889634);
+  const dim3 grid(Hkv * a.nchunk, B, num_splits);
+  switch (GH) {
+    case 1: return launch_scan_gh<1>(a, grid, stream);
+    case 2: return launch_scan_gh<2>(a, grid, stream);
+    case 4: return launch_scan_gh<4>(a, grid, stream);
+    default: return launch_scan_gh<8>(a, grid, stream);
+  }
+}
+
+}  // namespace gqa
+
+extern "C" int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cache,
+                                    const uint16_t* v_cache, const int* block_table,
+                                    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv,
+                                    int block_size, int max_blocks, float scale,
+                                    hipStream_t stream) {
+  hipError_t err = gqa::check_common(q, k_cache, v_cache, block_table, seq_lens, out, B, Hq, Hkv,
+                                     block_size, max_blocks);
+  if (err != hipSuccess) return err;
+  if (B == 0) return hipSuccess;
+  return gqa::launch_scan(q, k_cache, v_cache, block_table, seq_lens, out, nullptr, nullptr,
+                          nullptr, B, Hq, Hkv, block_size, max_blocks, scale, 1, stream);
+}
+
+extern "C" int gqa_decode_v2_partial_launch(const uint16_t* q, const uint16_t* k_cache,
+                                            const uint16_t* v_cache, const int* block_table,
+                                            const int* seq_lens, int B, int Hq, int Hkv,
+                                            int block_size, int max_blocks, float scale,
+                                            int num_splits, float* ws_acc, float* ws_m,
+                                            float* ws_l, hipStream_t stream) {
+  // `out` is not used by the partial kernel; pass ws_acc to the shared check.
+  hipError_t err = gqa::check_common(q, k_cache, v_cache, block_table, seq_lens, ws_acc, B, Hq,
+                                     Hkv, block_size, max_blocks);
+  if (err != hipSuccess) return err;
+  if (num_splits < 1 || num_splits > GQA_DECODE_MAX_SPLITS) return hipErrorInvalidValue;
+  if (B > 0 && (!ws_acc || !ws_m || !ws_l)) return hipErrorInvalidValue;
+  if (B == 0) return hipSuccess;
+  return gqa::launch_scan(q, k_cache, v_cache, block_table, seq_lens, nullptr, ws_acc, ws_m, ws_l,
+                          B, Hq, Hkv, block_size, max_blocks, scale, num_splits, stream);
+}
+
+extern "C" int gqa_decode_v2_merge_launch(const float* ws_acc, const float* ws_m,
+                                          const float* ws_l, uint16_t* out, int B, int Hq,
+                                          int num_splits, hipStream_t stream) {
+  if (B < 0 || Hq < 1 || (int64_t)B * Hq > (int64_t(1) << 30)) return hipErrorInvalidValue;
+  if (num_splits < 1 || num_splits > GQA_DECODE_MAX_SPLITS) return hipErrorInvalidValue;
+  if (B > 0 && (!ws_acc || !ws_m || !ws_l || !out)) return hipErrorInvalidValue;
+  if (B == 0) return hipSuccess;
+  const int BH = B * Hq;
+  hipLaunchKernelGGL(gqa::gqa_decode_merge_kernel, dim3((BH + 3) / 4), dim3(256), 0, stream,
+                     ws_acc, ws_m, ws_l, out, BH, num_splits);
+  return hipGetLastError();
+}
+
+extern "C" int gqa_decode_v2_launch(const uint16_t* q, const uint16_t* k_cache,
+                                    const uint16_t* v_cache, const int* block_table,
+                                    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv,
+                                    int block_size, int max_blocks, float scale, int num_splits,
+                                    float* ws_acc, float* ws_m, float* ws_l, hipStream_t stream) {
+  if (B > 0 && !out) return hipErrorInvalidValue;
+  const int err = gqa_decode_v2_partial_launch(q, k_cache, v_cache, block_table, seq_lens, B, Hq,
+                                               Hkv, block_size, max_blocks, scale, num_splits,
+                                               ws_acc, ws_m, ws_l, stream);
+  if (err != hipSuccess) return err;
+  return gqa_decode_v2_merge_launch(ws_acc, ws_m, ws_l, out, B, Hq, num_splits, stream);
+}
+
+extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
+  if (B <= 0 || Hq <= 0 || num_splits <= 0) return 0;
+  return (size_t)B * Hq * num_splits * (gqa::kHeadDim + 2) * sizeof(float);
+}
+
+// Number of splits: enough (b, kv-head chunk, split) workgroups that every CU
+// holds kTargetWgsPerCu of them, but no more splits than keep each wave at
+// kMinTilesPerWave tiles of the longest request (shorter splits only add
+// workspace traffic and merge work). The longest request is bounded by
+// max_blocks * block_size, the only length the host knows without reading
+// seq_lens back from the device.
+extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size, int max_blocks,
+                                          int num_cus) {
+  constexpr int kTargetWgsPerCu = 4;
+  constexpr int kMinTilesPerWave = 2;
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || block_size < 1 || max_blocks < 1) return 0;
+  if (num_cus <= 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        num_cus <= 0)
+      return 0;
+  }
+  const int G = Hq / Hkv;
+  const int GH = gqa::heads_per_wg(G);
+  const int64_t wgs1 = (int64_t)B * Hkv * ((G + GH - 1) / GH);
+  const int64_t target = (int64_t)num_cus * kTargetWgsPerCu;
+  int64_t ns = (target + wgs1 - 1) / wgs1;
+  const int64_t s_max = (int64_t)max_blocks * block_size;
+  const int64_t min_chunk = (int64_t)gqa::kTile * gqa::kWaves * kMinTilesPerWave;
+  const int64_t ns_len = s_max / min_chunk > 1 ? s_max / min_chunk : 1;
+  if (ns > ns_len) ns = ns_len;
+  if (ns > GQA_DECODE_MAX_SPLITS) ns = GQA_DECODE_MAX_SPLITS;
+  return ns < 1 ? 1 : (int)ns;
+}

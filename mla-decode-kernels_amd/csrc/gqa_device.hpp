@@ -1,0 +1,91 @@
+// Device helpers shared by the gfx950 GQA decode kernels: bf16 unpacking,
+// 16-lane DPP reductions, base-2 exponential, division by a runtime constant,
+// and the output normalisation every kernel ends with.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gqa {
+
+constexpr int kHeadDim = 128;
+constexpr float kNegInf = -__builtin_inff();
+// log2(e) and ln(2): the kernels evaluate exp(x) as 2^(x*log2(e)) on the
+// hardware base-2 exponential (v_exp_f32), the usual flash-decoding method.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// The two bf16 values packed in one 32-bit word, widened exactly to fp32.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16, round to nearest even (the rounding of __float2bfloat16 and of
+// torch's .to(torch.bfloat16)); NaN stays NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// acc += <a, b> over two packed bf16 pairs (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, true));
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row receives the
+// bitwise-identical total (each step adds a value to its mirror image, and fp
+// addition is commutative), so all lanes then take the same softmax path.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  return x;
+}
+
+// Sum over all 64 lanes, identical in every lane.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+// Hardware 2^x (v_exp_f32): 2^-inf = 0, 2^0 = 1.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Quotient n / d for 0 <= n < 2^31 and a divisor fixed at launch time, by the
+// round-up multiply-shift method (Granlund & Montgomery, PLDI 1994, sec. 4):
+// with l = ceil(log2 d) and mul = floor(2^32 (2^l - d) / d) + 1,
+// n / d == (umulhi(n, mul) + n) >> l.
+struct FastDiv {
+  uint32_t d, mul, shift;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint64_t mul = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)mul, l};
+}
+
+__device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
+// The single normalisation step every kernel finishes with (out = acc / l).
+// The single-pass and split-KV paths both call it, so a one-split merge (whose
+// factor is exactly 1) reproduces the single-pass output bit for bit.
+__device__ __forceinline__ float finalize(float acc, float l) { return acc / l; }
+
+}  // namespace gqa

@@ -1,0 +1,86 @@
+"""ctypes view of the C ABI in include/gqa_decode.h (libgqa_decode_hip.so).
+
+This is the binding a non-torch host would write; the
+tests use it to drive the launchers directly -- caller-owned workspace,
+error codes -- and to check that every declared entry point is exported.
+Pointer arguments take integers (e.g. ``tensor.data_ptr()``); the stream is a
+raw hipStream_t (``torch.cuda.current_stream().cuda_stream``).
+"""
+
+import ctypes
+import os
+import re
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "lib", "libgqa_decode_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "gqa_decode.h")
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_LAUNCH_ARGS = [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_float]
+
+_lib = None
+
+
+def declared_functions():
+    """Names of the functions include/gqa_decode.h declares."""
+    with open(HEADER_PATH) as f:
+        text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    pat = r"^\s*(?:GQA_DECODE_API\s+)?(?:int|size_t)\s+(gqa_decode_\w+)\s*\("
+    return sorted(set(re.findall(pat, text, flags=re.M)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} missing: run `python mla-decode-kernels_amd/build.py`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name in ("gqa_decode_v0_launch", "gqa_decode_v1_launch"):
+            fn = getattr(L, name)
+            fn.argtypes = _LAUNCH_ARGS + [_vp]
+            fn.restype = _i
+        L.gqa_decode_v2_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, _vp, _vp, _vp]
+        L.gqa_decode_v2_launch.restype = _i
+        L.gqa_decode_v2_partial_launch.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                                   ctypes.c_float, _i, _vp, _vp, _vp, _vp]
+        L.gqa_decode_v2_partial_launch.restype = _i
+        L.gqa_decode_v2_merge_launch.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+        L.gqa_decode_v2_merge_launch.restype = _i
+        L.gqa_decode_v2_workspace_bytes.argtypes = [_i, _i, _i]
+        L.gqa_decode_v2_workspace_bytes.restype = ctypes.c_size_t
+        L.gqa_decode_pick_num_splits.argtypes = [_i, _i, _i, _i, _i, _i]
+        L.gqa_decode_pick_num_splits.restype = _i
+        _lib = L
+    return _lib
+
+
+def v0_launch(*args):
+    return lib().gqa_decode_v0_launch(*args)
+
+
+def v1_launch(*args):
+    return lib().gqa_decode_v1_launch(*args)
+
+
+def v2_launch(*args):
+    return lib().gqa_decode_v2_launch(*args)
+
+
+def v2_partial_launch(*args):
+    return lib().gqa_decode_v2_partial_launch(*args)
+
+
+def v2_merge_launch(*args):
+    return lib().gqa_decode_v2_merge_launch(*args)
+
+
+def workspace_bytes(B, Hq, num_splits):
+    return lib().gqa_decode_v2_workspace_bytes(B, Hq, num_splits)
+
+
+def pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus):
+    return lib().gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus)

@@ -1,0 +1,163 @@
+// PyTorch-ROCm operator layer over the C ABI in include/gqa_decode.h.
+//
+// Mirrors the reference's python/gqa_decode_ext.cpp: the same three ops
+// (gqa_decode_v0/v1/v2), the same argument names and defaults (num_splits=8),
+// the same input checks with the same messages (:16-62), output and workspace
+// allocated from the caching allocator (:69, :105-109), launch on the current
+// stream (:70, :110). Additions: a device guard, num_splits == 0 selecting the
+// split-count heuristic (widening the accepted domain [1, 512] of :102-103),
+// a check of the launcher's return code, and one workspace allocation carved
+// into the three arrays instead of three.
+//
+// This file is host-only C++ (compiled by g++); all device code lives in the
+// hipcc-built libgqa_decode_hip.so it links against.
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include "gqa_decode.h"
+
+namespace {
+
+using launch_fn_t = int (*)(const uint16_t*, const uint16_t*, const uint16_t*, const int*,
+                            const int*, uint16_t*, int, int, int, int, int, float, hipStream_t);
+
+struct GqaDims {
+  int64_t B, Hq, Hkv, block_size, max_blocks;
+};
+
+GqaDims check_inputs(const torch::Tensor& q, const torch::Tensor& k_cache,
+                     const torch::Tensor& v_cache, const torch::Tensor& block_table,
+                     const torch::Tensor& seq_lens) {
+  TORCH_CHECK(q.is_cuda(), "q must be a CUDA tensor");
+  TORCH_CHECK(q.scalar_type() == torch::kBFloat16, "q must be bf16");
+  TORCH_CHECK(q.is_contiguous(), "q must be contiguous");
+  TORCH_CHECK(q.dim() == 3 && q.size(2) == 128, "q must be [B, Hq, 128]");
+
+  TORCH_CHECK(k_cache.is_cuda() && v_cache.is_cuda(), "k_cache/v_cache must be CUDA tensors");
+  TORCH_CHECK(k_cache.scalar_type() == torch::kBFloat16 &&
+                  v_cache.scalar_type() == torch::kBFloat16,
+              "k_cache/v_cache must be bf16");
+  TORCH_CHECK(k_cache.is_contiguous() && v_cache.is_contiguous(),
+              "k_cache/v_cache must be contiguous");
+  TORCH_CHECK(k_cache.dim() == 4 && k_cache.size(3) == 128,
+              "k_cache must be [num_blocks, block_size, Hkv, 128]");
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes(), "k_cache and v_cache must have the same shape");
+
+  TORCH_CHECK(block_table.is_cuda(), "block_table must be a CUDA tensor");
+  TORCH_CHECK(block_table.scalar_type() == torch::kInt32, "block_table must be int32");
+  TORCH_CHECK(block_table.is_contiguous(), "block_table must be contiguous");
+  TORCH_CHECK(block_table.dim() == 2, "block_table must be [B, max_blocks]");
+
+  TORCH_CHECK(seq_lens.is_cuda(), "seq_lens must be a CUDA tensor");
+  TORCH_CHECK(seq_lens.scalar_type() == torch::kInt32, "seq_lens must be int32");
+  TORCH_CHECK(seq_lens.is_contiguous(), "seq_lens must be contiguous");
+  TORCH_CHECK(seq_lens.dim() == 1, "seq_lens must be [B]");
+
+  const int64_t B = q.size(0);
+  const int64_t Hq = q.size(1);
+  const int64_t Hkv = k_cache.size(2);
+  const int64_t block_size = k_cache.size(1);
+  const int64_t max_blocks = block_table.size(1);
+  TORCH_CHECK(Hkv > 0 && Hq % Hkv == 0, "Hq must be divisible by Hkv");
+  TORCH_CHECK(block_table.size(0) == B, "block_table batch dim must match q");
+  TORCH_CHECK(seq_lens.size(0) == B, "seq_lens batch dim must match q");
+  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() &&
+                  q.device() == block_table.device() && q.device() == seq_lens.device(),
+              "all tensors must be on the same device");
+  return {B, Hq, Hkv, block_size, max_blocks};
+}
+
+const uint16_t* bf16_ptr(const torch::Tensor& t) {
+  return reinterpret_cast<const uint16_t*>(t.data_ptr());
+}
+
+void check_launch(int err, const char* op) {
+  TORCH_CHECK(err == 0, op, " failed: ", hipGetErrorString(static_cast<hipError_t>(err)),
+              " (hipError_t ", err, ")");
+}
+
+torch::Tensor gqa_decode_run(launch_fn_t launch, const char* op, const torch::Tensor& q,
+                             const torch::Tensor& k_cache, const torch::Tensor& v_cache,
+                             const torch::Tensor& block_table, const torch::Tensor& seq_lens,
+                             double scale) {
+  const GqaDims d = check_inputs(q, k_cache, v_cache, block_table, seq_lens);
+  const c10::DeviceGuard guard(q.device());
+  auto out = torch::empty_like(q);
+  hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+  check_launch(launch(bf16_ptr(q), bf16_ptr(k_cache), bf16_ptr(v_cache),
+                      block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+                      reinterpret_cast<uint16_t*>(out.data_ptr()), (int)d.B, (int)d.Hq,
+                      (int)d.Hkv, (int)d.block_size, (int)d.max_blocks, (float)scale, stream),
+               op);
+  return out;
+}
+
+torch::Tensor gqa_decode_v0(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                            torch::Tensor block_table, torch::Tensor seq_lens, double scale) {
+  return gqa_decode_run(gqa_decode_v0_launch, "gqa_decode_v0_launch", q, k_cache, v_cache,
+                        block_table, seq_lens, scale);
+}
+
+torch::Tensor gqa_decode_v1(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                            torch::Tensor block_table, torch::Tensor seq_lens, double scale) {
+  return gqa_decode_run(gqa_decode_v1_launch, "gqa_decode_v1_launch", q, k_cache, v_cache,
+                        block_table, seq_lens, scale);
+}
+
+int64_t pick_num_splits(const GqaDims& d, const torch::Tensor& q) {
+  int cus = 0;
+  const int dev = q.device().index();
+  TORCH_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess,
+              "could not query the CU count of device ", dev);
+  return gqa_decode_pick_num_splits((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
+                                    (int)d.max_blocks, cus);
+}
+
+torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                            torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                            int64_t num_splits) {
+  const GqaDims d = check_inputs(q, k_cache, v_cache, block_table, seq_lens);
+  TORCH_CHECK(num_splits >= 0 && num_splits <= GQA_DECODE_MAX_SPLITS,
+              "num_splits must be in [1, 512] (or 0 for the heuristic)");
+  const c10::DeviceGuard guard(q.device());
+  if (num_splits == 0) num_splits = d.B > 0 ? pick_num_splits(d, q) : 1;
+  TORCH_CHECK(num_splits >= 1, "num_splits heuristic failed");
+
+  auto out = torch::empty_like(q);
+  auto f32 = torch::TensorOptions().dtype(torch::kFloat32).device(q.device());
+  const int64_t states = d.B * d.Hq * num_splits;
+  auto ws = torch::empty({states * (128 + 2)}, f32);
+  float* ws_acc = ws.data_ptr<float>();
+  float* ws_m = ws_acc + states * 128;
+  float* ws_l = ws_m + states;
+  hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+  check_launch(gqa_decode_v2_launch(bf16_ptr(q), bf16_ptr(k_cache), bf16_ptr(v_cache),
+                                    block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+                                    reinterpret_cast<uint16_t*>(out.data_ptr()), (int)d.B,
+                                    (int)d.Hq, (int)d.Hkv, (int)d.block_size, (int)d.max_blocks,
+                                    (float)scale, (int)num_splits, ws_acc, ws_m, ws_l, stream),
+               "gqa_decode_v2_launch");
+  return out;
+}
+
+int64_t gqa_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t block_size,
+                              int64_t max_blocks, int64_t num_cus) {
+  return gqa_decode_pick_num_splits((int)B, (int)Hq, (int)Hkv, (int)block_size, (int)max_blocks,
+                                    (int)num_cus);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("gqa_decode_v0", &gqa_decode_v0, "GQA decode v0 naive kernel (paged KV, bf16)");
+  m.def("gqa_decode_v1", &gqa_decode_v1, "GQA decode v1 single-pass kernel (paged KV, bf16)");
+  m.def("gqa_decode_v2", &gqa_decode_v2, "GQA decode v2 split-KV kernel (paged KV, bf16)",
+        py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"),
+        py::arg("seq_lens"), py::arg("scale"), py::arg("num_splits") = 8);
+  m.def("num_splits_heuristic", &gqa_decode_num_splits,
+        "gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus)",
+        py::arg("B"), py::arg("Hq"), py::arg("Hkv"), py::arg("block_size"),
+        py::arg("max_blocks"), py::arg("num_cus") = 0);
+}

@@ -1,0 +1,165 @@
+"""CPU tests of the drop-in boundary: the C ABI library and the torch operator
+layer, without launching anything (this container has no GPU).
+
+Covers: every function include/gqa_decode.h declares is exported; the
+workspace-size and split-count entry points; argument rejection before any
+launch (hipErrorInvalidValue); the torch op's input checks and messages
+(python/gqa_decode_ext.cpp:16-62,102-103 of the reference).
+"""
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+import capi
+
+INVALID = capi.HIP_ERROR_INVALID_VALUE
+
+
+def test_library_exports_every_declared_function():
+    declared = capi.declared_functions()
+    assert declared == sorted([
+        "gqa_decode_v0_launch", "gqa_decode_v1_launch", "gqa_decode_v2_launch",
+        "gqa_decode_v2_partial_launch", "gqa_decode_v2_merge_launch",
+        "gqa_decode_v2_workspace_bytes", "gqa_decode_pick_num_splits",
+    ])
+    lib = capi.lib()
+    for name in declared:
+        assert hasattr(lib, name), f"{name} not exported"
+
+
+def test_library_exports_nothing_else():
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    names = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    assert {n for n in names if n.startswith("gqa")} == set(capi.declared_functions())
+
+
+@pytest.mark.parametrize("B,Hq,ns", [(32, 32, 8), (1, 32, 1), (128, 64, 512), (3, 5, 7)])
+def test_workspace_bytes(B, Hq, ns):
+    assert capi.workspace_bytes(B, Hq, ns) == B * Hq * ns * (128 + 2) * 4
+
+
+@pytest.mark.parametrize("args", [(0, 32, 8), (32, 0, 8), (32, 32, 0), (-1, 32, 8)])
+def test_workspace_bytes_invalid(args):
+    assert capi.workspace_bytes(*args) == 0
+
+
+def test_pick_num_splits_properties():
+    cus = 256
+    # Representative shape: fills every CU, splits stay long.
+    ns = capi.pick_num_splits(32, 32, 8, 16, 512, cus)
+    assert 1 <= ns <= 512
+    assert 32 * 8 * ns >= cus
+    assert math.ceil(8192 / ns) >= 128
+    # Fewer requests -> at least as many splits.
+    prev = 0
+    for B in (128, 32, 8, 1):
+        cur = capi.pick_num_splits(B, 32, 8, 64, 512, cus)
+        assert cur >= prev
+        prev = cur
+    # Very short sequences are not split below the minimum split length.
+    assert capi.pick_num_splits(1, 32, 8, 16, 1, cus) == 1
+    assert capi.pick_num_splits(1, 32, 8, 16, 8, cus) == 1
+    # Never above the kernel's limit.
+    assert capi.pick_num_splits(1, 8, 8, 64, 1 << 20, 100000) == 512
+    # Enough work already: no split.
+    assert capi.pick_num_splits(4096, 32, 8, 16, 64, cus) == 1
+
+
+@pytest.mark.parametrize("args", [(0, 32, 8, 16, 512, 256), (32, 30, 8, 16, 512, 256),
+                                  (32, 32, 0, 16, 512, 256), (32, 32, 8, 0, 512, 256),
+                                  (32, 32, 8, 16, 0, 256)])
+def test_pick_num_splits_invalid(args):
+    assert capi.pick_num_splits(*args) == 0
+
+
+FAKE = 0x1000  # never dereferenced: every call below is rejected before a launch
+
+
+def launch_args(**over):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, bt=FAKE, sl=FAKE, out=FAKE, B=2, Hq=32, Hkv=8, bs=16,
+             max_blocks=4, scale=0.088)
+    a.update(over)
+    return [a[k] for k in ("q", "k", "v", "bt", "sl", "out", "B", "Hq", "Hkv", "bs",
+                           "max_blocks", "scale")]
+
+
+BAD = [dict(Hq=30), dict(Hkv=0), dict(Hq=0), dict(bs=0), dict(max_blocks=0), dict(B=-1),
+       dict(B=70000), dict(q=None), dict(k=None), dict(v=None), dict(bt=None), dict(sl=None),
+       dict(out=None), dict(bs=1 << 20, Hkv=64)]
+
+
+@pytest.mark.parametrize("over", BAD)
+def test_launchers_reject_bad_arguments(over):
+    args = launch_args(**over)
+    assert capi.v0_launch(*args, None) == INVALID
+    assert capi.v1_launch(*args, None) == INVALID
+    assert capi.v2_launch(*args, 8, FAKE, FAKE, FAKE, None) == INVALID
+
+
+@pytest.mark.parametrize("ns", [0, -1, 513])
+def test_v2_rejects_num_splits(ns):
+    assert capi.v2_launch(*launch_args(), ns, FAKE, FAKE, FAKE, None) == INVALID
+    assert capi.v2_partial_launch(*launch_args()[:5], *launch_args()[6:], ns, FAKE, FAKE, FAKE,
+                                  None) == INVALID
+    assert capi.v2_merge_launch(FAKE, FAKE, FAKE, FAKE, 2, 32, ns, None) == INVALID
+
+
+@pytest.mark.parametrize("which", [0, 1, 2])
+def test_v2_rejects_missing_workspace(which):
+    ws = [FAKE, FAKE, FAKE]
+    ws[which] = None
+    assert capi.v2_launch(*launch_args(), 8, *ws, None) == INVALID
+    assert capi.v2_merge_launch(*ws, FAKE, 2, 32, 8, None) == INVALID
+
+
+def test_empty_batch_is_a_no_op():
+    args = launch_args(B=0, q=None, k=None, v=None, bt=None, sl=None, out=None)
+    assert capi.v0_launch(*args, None) == capi.HIP_SUCCESS
+    assert capi.v1_launch(*args, None) == capi.HIP_SUCCESS
+    assert capi.v2_launch(*args, 8, None, None, None, None) == capi.HIP_SUCCESS
+
+
+# ----------------------------------------------------------- torch operator
+
+
+@pytest.fixture(scope="module")
+def binding():
+    import binding as b
+    return b
+
+
+def cpu_case(B=2, Hq=32, Hkv=8, bs=16, nb=8, mb=4):
+    q = torch.zeros(B, Hq, 128, dtype=torch.bfloat16)
+    k = torch.zeros(nb, bs, Hkv, 128, dtype=torch.bfloat16)
+    bt = torch.zeros(B, mb, dtype=torch.int32)
+    sl = torch.ones(B, dtype=torch.int32)
+    return q, k, k.clone(), bt, sl
+
+
+def test_binding_exports(binding):
+    assert set(binding.KERNELS) == {"v0", "v1", "v2"}
+    assert binding.KERNELS["v2"] is binding.gqa_decode_v2
+    assert binding.EXTENSION_PATH.startswith(capi._PKG_DIR)
+    assert binding.num_splits_heuristic(32, 32, 8, 16, 512, 256) == \
+        capi.pick_num_splits(32, 32, 8, 16, 512, 256)
+
+
+@pytest.mark.parametrize("kernel", ["v0", "v1", "v2"])
+def test_op_rejects_host_tensors(binding, kernel):
+    with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
+        binding.KERNELS[kernel](*cpu_case(), 0.088)
+
+
+def test_op_check_order_and_messages(binding):
+    # Checks run in the reference's order, so the first failing one names it.
+    q, k, v, bt, sl = cpu_case()
+    with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
+        binding.gqa_decode_v2(q.float(), k, v, bt, sl, 0.088, num_splits=4)
+    with pytest.raises(TypeError):
+        binding.gqa_decode_v2(q, k, v, bt, sl, 0.088, num_splits="x")
