@@ -9,12 +9,15 @@ d=128, S=8192, B=32, block=16: 1 GiB of K+V), the shape the headline metric is
 quoted on; the other configs are selectable with --config.
 
 Timed region: W untimed steps, then K steps bracketed by
-torch.cuda.synchronize(). Each v2 step is the C ABI's partial launch followed
-by its merge launch on the current stream, with a caller-owned workspace, and
-HIP events before, between and after them:
-  value (median us)        median of the per-step event intervals
-  roofline.achieved        algorithmic KV bytes / mean partial-kernel interval
+torch.cuda.synchronize(). A v2 step is the C ABI's partial launch followed by
+its merge launch (one launch when num_splits is 1) on the current stream, with
+a caller-owned workspace. HIP events are recorded only between groups of steps
+(an event between two kernels delays the second):
+  value (median us)        median over the groups of the per-step average
   ms_per_step              host wall time of the K steps / K
+  roofline.achieved        algorithmic KV bytes / the dominant (partial)
+                           kernel's average duration over K back-to-back
+                           launches, events around the whole run
 The torch operator (what Python callers use, allocation included) is timed
 too, the reference's way (bench/common.py:49-64: events around each call,
 synchronize after each), as `op_median_us`.
@@ -29,7 +32,6 @@ import argparse
 import json
 import math
 import os
-import subprocess
 import sys
 import time
 
@@ -59,6 +61,10 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="oracle threads (default: min(16, cpu count))")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="instead: time a plain device copy of MIB MiB (torch.neg into a second "
+                         "buffer), the known-size kernel that calibrates rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args(argv)
 
 
@@ -77,21 +83,23 @@ def read_traffic(config, kernel, num_splits):
 
 
 def gpu_clocks():
-    try:
-        out = subprocess.run(["amd-smi", "metric", "--clock", "--json"], capture_output=True,
-                             text=True, timeout=20)
-        if out.returncode == 0:
-            data = json.loads(out.stdout)
-            entry = data[0] if isinstance(data, list) else data
-            clk = entry.get("clock", entry)
-            pick = {}
-            for key in ("gfx_0", "mem_0"):
-                if key in clk and isinstance(clk[key], dict):
-                    pick[key] = clk[key].get("clk", clk[key])
-            return pick or "unparsed"
-    except Exception as e:  # noqa: BLE001 - clocks are informational only
-        return f"unavailable: {type(e).__name__}"
-    return "unavailable"
+    """Current shader and memory clocks from the amdgpu sysfs DPM tables (the
+    entry marked '*'); read directly so no helper process is started."""
+    import glob
+
+    out = {}
+    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
+        for key, fname in (("sclk", "pp_dpm_sclk"), ("mclk", "pp_dpm_mclk")):
+            try:
+                with open(os.path.join(dev, fname)) as f:
+                    cur = [ln.split(":", 1)[1].strip(" *\n") for ln in f if ln.rstrip().endswith("*")]
+                if cur:
+                    out.setdefault(key, cur[0])
+            except OSError:
+                pass
+        if out:
+            break
+    return out or "unavailable"
 
 
 def main(argv=None):
@@ -114,6 +122,15 @@ def main(argv=None):
         return 1
     dev = torch.device("cuda", 0)
     props = torch.cuda.get_device_properties(dev)
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        x = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        ms = cases.time_op(lambda: torch.neg(x, out=y), warmup=3, runs=10)
+        print(json.dumps({"copy_probe": "torch.neg fp32", "read_bytes": n, "write_bytes": n,
+                          "median_us": round(ms * 1e3, 2),
+                          "gbps_read_plus_write": round(2 * n / ms / 1e6, 1)}), flush=True)
+        return 0
     cfg = cases.CONFIGS[args.config]
     S_list = cases.config_seq_lens(args.config, args.seed)
     kvb = cases.kv_bytes(S_list, cfg["Hkv"])
@@ -143,7 +160,11 @@ def main(argv=None):
     ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr())
 
     def step_parts():
-        """One step as its kernel launches (C ABI), for the event timeline."""
+        """One step as its kernel launches through the C ABI."""
+        if args.kernel == "v2" and ns == 1:
+            # One split: the single-pass kernel writes out (and the workspace).
+            return [lambda: capi.v2_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, 1,
+                                           ws_acc, ws_m, ws_l, sp)]
         if args.kernel == "v2":
             return [lambda: capi.v2_partial_launch(*ptrs, B, Hq, Hkv, bs, mb, scale, ns, ws_acc,
                                                    ws_m, ws_l, sp),
@@ -153,30 +174,50 @@ def main(argv=None):
         return [lambda: launch(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, sp)]
 
     parts = step_parts()
-    for _ in range(args.warmup):
+
+    def step():
         for p in parts:
-            assert p() == 0
+            rc = p()
+            if rc != 0:
+                raise RuntimeError(f"launch failed: hipError_t {rc}")
+
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
 
+    # Timed region: exactly K steps back to back. Events sit only between
+    # groups of steps (an event between two kernels delays the second one), so
+    # each group's average is the steady-state step time; value = their median.
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)] for _ in range(K)]
+    groups = max(1, min(10, K // 5))
+    bounds = [round(g * K / groups) for g in range(groups + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    for i in range(K):
-        ev[i][0].record(stream)
-        for j, p in enumerate(parts):
-            rc = p()
-            ev[i][j + 1].record(stream)
-        if rc != 0:
-            raise RuntimeError(f"launch failed: hipError_t {rc}")
+    for g in range(groups):
+        ev[g].record(stream)
+        for _ in range(bounds[g + 1] - bounds[g]):
+            step()
+    ev[groups].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    step_us = sorted(ev[i][0].elapsed_time(ev[i][-1]) * 1e3 for i in range(K))
-    kern_us = [ev[i][0].elapsed_time(ev[i][1]) * 1e3 for i in range(K)]
-    median_us = step_us[K // 2]
-    kern_avg_us = sum(kern_us) / K
-    log(f"{args.kernel}: median step {median_us:.2f} us, dominant kernel avg {kern_avg_us:.2f} us "
-        f"({kvb / kern_avg_us / 1e3:.1f} GB/s), wall {wall / K * 1e3:.3f} ms/step")
+    group_us = sorted(ev[g].elapsed_time(ev[g + 1]) * 1e3 / (bounds[g + 1] - bounds[g])
+                      for g in range(groups))
+    median_us = group_us[groups // 2]
+
+    # The dominant kernel alone, K launches back to back on the same stream:
+    # its average launch duration for the roofline.
+    kev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    kev[0].record(stream)
+    for _ in range(K):
+        if parts[0]() != 0:
+            raise RuntimeError("launch failed")
+    kev[1].record(stream)
+    torch.cuda.synchronize()
+    kern_avg_us = kev[0].elapsed_time(kev[1]) * 1e3 / K
+    log(f"{args.kernel}: median step {median_us:.2f} us (groups {group_us[0]:.1f}..{group_us[-1]:.1f}), "
+        f"dominant kernel avg {kern_avg_us:.2f} us ({kvb / kern_avg_us / 1e3:.1f} GB/s), "
+        f"wall {wall / K * 1e3:.3f} ms/step")
 
     # The torch operator, timed the reference's way.
     if args.kernel == "v2":

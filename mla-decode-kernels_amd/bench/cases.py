@@ -41,7 +41,7 @@ def config_seq_lens(name, seed=0):
 
 
 def make_case(S_list, Hq, Hkv, bs, *, pool=None, pool_factor=None, seed=0, device="cuda",
-              qkv_std=1.0, poison=False, max_blocks=None):
+              qkv_std=1.0, poison=False, max_blocks=None, shuffle=True):
     """Build (q, k_cache, v_cache, block_table, seq_lens) on `device`.
 
     q/k/v ~ qkv_std * N(0, 1) in bf16 from a seeded generator on `device`.
@@ -49,7 +49,8 @@ def make_case(S_list, Hq, Hkv, bs, *, pool=None, pool_factor=None, seed=0, devic
     or exactly the needed count); block ids come from a seeded CPU permutation
     of the pool, request b taking the next ceil(S_b / bs) ids. Entries past a
     request's blocks are -1. With poison=True every unallocated block and every
-    slot past S_b in a request's last block is NaN.
+    slot past S_b in a request's last block is NaN. shuffle=False hands out
+    the pool in order (request b's blocks contiguous in memory).
     """
     B = len(S_list)
     n_blocks = [(int(s) + bs - 1) // bs for s in S_list]
@@ -74,7 +75,8 @@ def make_case(S_list, Hq, Hkv, bs, *, pool=None, pool_factor=None, seed=0, devic
             x = torch.randn(n, bs, Hkv, D, device=device, generator=gen, dtype=torch.float32)
             cache[i:i + n] = (x * qkv_std).to(torch.bfloat16)
 
-    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed))
+    perm = (torch.randperm(pool, generator=torch.Generator().manual_seed(seed)) if shuffle
+            else torch.arange(pool))
     block_table = torch.full((B, max_blocks), -1, dtype=torch.int32)
     used = torch.zeros(pool, dtype=torch.bool)
     off = 0
@@ -100,12 +102,12 @@ def make_case(S_list, Hq, Hkv, bs, *, pool=None, pool_factor=None, seed=0, devic
     return q, k_cache, v_cache, block_table.to(device), seq_lens
 
 
-def make_config_case(name, seed=0, device="cuda", poison=False):
+def make_config_case(name, seed=0, device="cuda", poison=False, shuffle=True):
     cfg = CONFIGS[name]
     S_list = config_seq_lens(name, seed)
     return make_case(S_list, cfg["Hq"], cfg["Hkv"], cfg["bs"], pool=cfg.get("pool"),
                      pool_factor=cfg.get("pool_factor"), seed=seed, device=device,
-                     poison=poison)
+                     poison=poison, shuffle=shuffle)
 
 
 def kv_bytes(S_list, Hkv):

@@ -1,21 +1,21 @@
 // v1 (single pass) and v2 (split-KV partial + log-sum-exp merge) decode
 // kernels for gfx950.
 //
-// Work decomposition. One workgroup of kWaves wave64s owns one
-// (b, kv-head, q-head chunk, split) and serves every q-head of the GQA group
-// from the same K/V registers, so each K/V row crosses HBM once (the
-// reference's per-q-head CTAs rely on L2 for that: kernels/gqa_decode/
-// v2_splitkv.cu:18-24). Tiles of 16 tokens are dealt round-robin to the waves
-// of the workgroup. Inside a wave the 64 lanes form 4 DPP rows of 16 lanes; a
-// row reads one 256-byte K (or V) head row with 16-byte loads, so one load
-// instruction covers 4 tokens and a tile is 4 K loads + 4 V loads per lane.
+// Work decomposition. A workgroup of P wave64s owns one kv-head of one request
+// (and one split in v2) and serves every q-head of its GQA group from the same
+// K/V registers, so each K/V row crosses HBM once (the reference's per-q-head
+// CTAs rely on L2 for that: kernels/gqa_decode/v2_splitkv.cu:18-24). The P
+// waves deal the segment's 16-token tiles round-robin. The 64 lanes of a wave
+// form 4 DPP rows of 16 lanes; a row reads one 256-byte K (or V) head row with
+// 16-byte loads, so one load instruction covers 4 tokens and a tile is 4 K
+// loads + 4 V loads per lane.
 //
 // Per tile: QK^T with v_dot2c_f32_bf16 on the packed bf16 q and K words, a
 // 4-step DPP row reduction, then one online-softmax update per (row, head) for
 // the whole tile (max over its 4 tokens, one rescale of l and acc) in base-2
 // units, and PV as fp32 FMAs. The next tile's loads are issued before the
-// current tile is consumed. At the end the 4 row states of a wave and then the
-// kWaves wave states are merged in a fixed order (bitwise deterministic).
+// current tile is consumed. At the end the row states of each wave and then
+// the P wave states are merged in a fixed order: bitwise deterministic.
 //
 // Split rule: segment `split` of request b covers
 // [split*chunk, min(S, (split+1)*chunk)) with chunk = ceil(S/num_splits)
@@ -24,6 +24,8 @@
 // block_size is a multiple of 16, which lets the block id be a scalar load.
 // Splits past the end of a short request are empty and store the neutral
 // state (-inf, 0, 0), whose merge factor is 0 (v2_splitkv.cu:33-40).
+// num_splits == 1 runs the single-pass kernel, so v2 with one split equals v1
+// bit for bit.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
 #include "gqa_decode.h"
@@ -32,7 +34,21 @@ namespace gqa {
 
 constexpr int kTile = 16;   // tokens per wave per tile
 constexpr int kLoads = 4;   // 16-byte K loads (and V loads) per lane per tile
-constexpr int kWaves = 4;   // waves per workgroup
+
+// Launch shapes. A workgroup holds P waves that share one kv-head of one
+// request and split, take its 16-token tiles round-robin and merge their
+// states through LDS. Measured on MI355X: the stream runs fastest with about
+// one wave per SIMD resident (4 per CU), each keeping one tile in flight while
+// it consumes the previous one; more resident waves or deeper prefetch only add
+// queueing. P = 4 waves per kv-head keeps a workgroup's reads adjacent and the
+// merge in LDS; 8-head groups (GH = 8) run P = 1 to stay within 256 VGPRs at
+// two waves per SIMD, which their larger VALU share needs.
+constexpr int kWavesPerHead = 4;      // P for GH <= 4 (and every single-pass launch)
+constexpr int kWavesPerHeadGH8 = 1;   // P for GH = 8 split launches
+constexpr int kScanDepth = 2;         // register tiles in flight per wave
+inline int waves_per_head(int GH, int num_splits) {
+  return (GH == 8 && num_splits > 1) ? kWavesPerHeadGH8 : kWavesPerHead;
+}
 
 struct ScanArgs {
   const uint16_t* q;
@@ -54,16 +70,21 @@ struct TileRegs {
   uint4 v[kLoads];
 };
 
-template <int GH, bool kBlockUniform>
-__global__ __launch_bounds__(64 * kWaves) void gqa_decode_scan_kernel(const ScanArgs a) {
+// One workgroup = P waves on one kv-head of one request b, one q-head chunk of
+// GH heads and one split; wave w takes tiles w, w + P, ... of the segment.
+// Single-pass launches (num_splits == 1) with `out` set write the normalised
+// output; with the workspace set they write the unnormalised state (both
+// when both are set).
+template <int GH, int P, int DEPTH, bool kBlockUniform>
+__global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs a) {
   const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane >> 4;  // DPP row: token 4j + r of each load j
   const int c = lane & 15;  // dims [8c, 8c + 8)
   const int hkv = blockIdx.x / a.nchunk;
   const int hc = blockIdx.x - hkv * a.nchunk;
   const int b = blockIdx.y, split = blockIdx.z;
-  const int h0 = hkv * a.G + hc * GH;  // first q-head of this chunk
+  const int h0 = hkv * a.G + hc * GH;  // first q-head of this wave
   const int nh = min(GH, a.G - hc * GH);
 
   const int S = max(a.seq_lens[b], 0);
@@ -72,7 +93,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_scan_kernel(const Scan
   const int seg_start = min(split * chunk, S);
   const int seg_end = min(S, seg_start + chunk);
   const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
-  const int my_tiles = ntiles > wv ? (ntiles - wv + kWaves - 1) / kWaves : 0;
+  const int my_tiles = ntiles > ph ? (ntiles - ph + P - 1) / P : 0;
 
   uint4 qf[GH];
 #pragma unroll
@@ -97,7 +118,7 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_scan_kernel(const Scan
   const int* bt = a.block_table + (size_t)b * a.max_blocks;
   const int bs = a.block_size;
 
-  auto tile_start = [&](int k) { return seg_start + kTile * (wv + kWaves * k); };
+  auto tile_start = [&](int k) { return seg_start + kTile * (ph + P * k); };
 
   // Issue the K and V loads of this wave's tile k. Tokens at or past seg_end
   // read the tile's first token instead (always valid), so no load touches an
@@ -175,32 +196,43 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_scan_kernel(const Scan
     }
   };
 
-  // Two register tiles in flight: the loop body issues tile k+1 (k+2) before
-  // consuming tile k (k+1) and has no branch, so the wait before each consume
-  // covers only the tile being consumed.
+  // DEPTH register tiles in flight. The steady-state loop body issues tile
+  // k + DEPTH - 1 before consuming tile k and has no branch, so the wait before
+  // each consume covers only the tile being consumed.
   if (my_tiles > 0) {
-    TileRegs t0, t1;
-    issue(0, t0);
+    TileRegs t[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i)
+      if (i < my_tiles) issue(i, t[i]);
     int k = 0;
-    for (; k + 2 < my_tiles; k += 2) {
-      issue(k + 1, t1);
-      consume(k, t0);
-      issue(k + 2, t0);
-      consume(k + 1, t1);
+    for (; k + 2 * DEPTH - 2 < my_tiles; k += DEPTH) {
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
+        consume(k + i, t[i]);
+      }
     }
-    if (k + 1 < my_tiles) {
-      issue(k + 1, t1);
-      consume(k, t0);
-      consume(k + 1, t1);
-    } else {
-      consume(k, t0);
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) {
+      if (k + i < my_tiles) {
+        if (k + i + DEPTH - 1 < my_tiles) issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
+        consume(k + i, t[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) {
+      // At most 2*DEPTH - 2 tiles remain after the loop; the block above
+      // consumed DEPTH of them.
+      if (k + DEPTH + i < my_tiles) {
+        if (k + DEPTH + i + DEPTH - 1 < my_tiles)
+          issue(k + DEPTH + i + DEPTH - 1, t[(i + 2 * DEPTH - 1) % DEPTH]);
+        consume(k + DEPTH + i, t[(DEPTH + i) % DEPTH]);
+      }
     }
   }
 
   // Merge the 4 row states of the wave (every row ends with the same totals).
-  __shared__ float lds_m[kWaves][GH];
-  __shared__ float lds_l[kWaves][GH];
-  __shared__ float lds_acc[kWaves][GH][kHeadDim];
+  float Mw[GH], Lw[GH];
 #pragma unroll
   for (int h = 0; h < GH; ++h) {
     const float mr = m[h];
@@ -217,48 +249,83 @@ __global__ __launch_bounds__(64 * kWaves) void gqa_decode_scan_kernel(const Scan
       x += __shfl_xor(x, 32, 64);
       acc[h][d] = x;
     }
-    if (r == 0) {
-      float4* dst = reinterpret_cast<float4*>(&lds_acc[wv][h][8 * c]);
-      dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-    }
-    if (lane == 0) {
-      lds_m[wv][h] = M;
-      lds_l[wv][h] = lr;
-    }
+    Mw[h] = M;
+    Lw[h] = lr;
   }
-  __syncthreads();
 
-  // Merge the wave states in wave order and write the result.
-  for (int idx = threadIdx.x; idx < GH * kHeadDim; idx += 64 * kWaves) {
-    const int h = idx / kHeadDim, d = idx % kHeadDim;
-    if (h >= nh) continue;
-    float M = lds_m[0][h];
+  if constexpr (P == 1) {
+    // The wave holds the whole state of its kv-head: row 0 writes it.
+    if (r == 0) {
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds_m[w][h]);
-    const float Ms = M == kNegInf ? 0.f : M;
-    float L = 0.f, A = 0.f;
+      for (int h = 0; h < GH; ++h) {
+        if (h >= nh) continue;
+        const size_t bh = (size_t)b * a.Hq + h0 + h;
+        if (a.out) {
+          uint32_t w[4];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = lds_m[w][h];
-      const float f = mw == M ? 1.f : exp2_fast(mw - Ms);
-      if (w == 0) {
-        L = lds_l[0][h] * f;
-        A = lds_acc[0][h][d] * f;
-      } else {
-        L = fmaf(lds_l[w][h], f, L);
-        A = fmaf(lds_acc[w][h][d], f, A);
+          for (int d = 0; d < 4; ++d)
+            w[d] = f32_to_bf16_bits(finalize(acc[h][2 * d], Lw[h])) |
+                   (f32_to_bf16_bits(finalize(acc[h][2 * d + 1], Lw[h])) << 16);
+          *reinterpret_cast<uint4*>(a.out + bh * kHeadDim + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        if (a.ws_acc) {
+          const size_t st = bh * ns + split;
+          float4* dst = reinterpret_cast<float4*>(a.ws_acc + st * kHeadDim + 8 * c);
+          dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+          dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+          if (c == 0) {
+            a.ws_m[st] = Mw[h] * kLn2;  // back to natural-log units
+            a.ws_l[st] = Lw[h];
+          }
+        }
       }
     }
-    const size_t bh = (size_t)b * a.Hq + h0 + h;
-    if (a.out) {
-      a.out[bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(finalize(A, L));
-    } else {
-      const size_t st = bh * ns + split;
-      a.ws_acc[st * kHeadDim + d] = A;
-      if (d == 0) {
-        a.ws_m[st] = M * kLn2;  // back to natural-log units
-        a.ws_l[st] = L;
+  } else {
+    // P waves share the kv-head: merge their states through LDS in wave order.
+    __shared__ float lds_m[P][GH];
+    __shared__ float lds_l[P][GH];
+    __shared__ float lds_acc[P][GH][kHeadDim];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      if (r == 0) {
+        float4* dst = reinterpret_cast<float4*>(&lds_acc[ph][h][8 * c]);
+        dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+      }
+      if (lane == 0) {
+        lds_m[ph][h] = Mw[h];
+        lds_l[ph][h] = Lw[h];
+      }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nh * kHeadDim; idx += 64 * P) {
+      const int h = idx / kHeadDim, d = idx % kHeadDim;
+      float M = lds_m[0][h];
+#pragma unroll
+      for (int w = 1; w < P; ++w) M = fmaxf(M, lds_m[w][h]);
+      const float Ms = M == kNegInf ? 0.f : M;
+      float L = 0.f, A = 0.f;
+#pragma unroll
+      for (int w = 0; w < P; ++w) {
+        const float mw = lds_m[w][h];
+        const float f = mw == M ? 1.f : exp2_fast(mw - Ms);
+        if (w == 0) {
+          L = lds_l[0][h] * f;
+          A = lds_acc[0][h][d] * f;
+        } else {
+          L = fmaf(lds_l[w][h], f, L);
+          A = fmaf(lds_acc[w][h][d], f, A);
+        }
+      }
+      const size_t bh = (size_t)b * a.Hq + h0 + h;
+      if (a.out) a.out[bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(finalize(A, L));
+      if (a.ws_acc) {
+        const size_t st = bh * ns + split;
+        a.ws_acc[st * kHeadDim + d] = A;
+        if (d == 0) {
+          a.ws_m[st] = M * kLn2;  // back to natural-log units
+          a.ws_l[st] = L;
+        }
       }
     }
   }
@@ -298,18 +365,27 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(const float* __re
   reinterpret_cast<uint32_t*>(out + (size_t)bh * kHeadDim)[lane] = lo | (hi << 16);
 }
 
-// q-heads served per workgroup: the whole group up to 8, rounded up to a power
-// of two (extra heads carry q = 0 and are not written); larger groups are cut
-// into chunks of 8 that each scan the same K/V.
-inline int heads_per_wg(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+// q-heads served per wave: the whole group up to 8, rounded up to a power of
+// two (extra heads carry q = 0 and are not written); larger groups are cut into
+// chunks of 8 that each scan the same K/V.
+inline int heads_per_wave(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+
+template <int GH, int P>
+hipError_t launch_scan_shape(const ScanArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.block_size % kTile == 0)
+    hipLaunchKernelGGL((gqa_decode_scan_kernel<GH, P, kScanDepth, true>), grid, dim3(64 * P), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((gqa_decode_scan_kernel<GH, P, kScanDepth, false>), grid, dim3(64 * P), 0,
+                       stream, a);
+  return hipGetLastError();
+}
 
 template <int GH>
-hipError_t launch_scan_gh(const ScanArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.block_size % kTile == 0)
-    hipLaunchKernelGGL((gqa_decode_scan_kernel<GH, true>), grid, dim3(64 * kWaves), 0, stream, a);
-  else
-    hipLaunchKernelGGL((gqa_decode_scan_kernel<GH, false>), grid, dim3(64 * kWaves), 0, stream, a);
-  return hipGetLastError();
+hipError_t launch_scan_gh(const ScanArgs& a, int B, hipStream_t stream) {
+  const dim3 grid(a.Hkv * a.nchunk, B, a.num_splits);
+  if (waves_per_head(GH, a.num_splits) == 1) return launch_scan_shape<GH, 1>(a, grid, stream);
+  return launch_scan_shape<GH, kWavesPerHead>(a, grid, stream);
 }
 
 hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -329,19 +405,18 @@ hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_
   a.Hq = Hq;
   a.Hkv = Hkv;
   a.G = Hq / Hkv;
-  const int GH = heads_per_wg(a.G);
+  const int GH = heads_per_wave(a.G);
   a.nchunk = (a.G + GH - 1) / GH;
   a.block_size = block_size;
   a.max_blocks = max_blocks;
   a.num_splits = num_splits;
   a.bs_div = make_fastdiv((uint32_t)block_size);
   a.scale_log2e = (float)((double)scale * 1.4426950408889634);
-  const dim3 grid(Hkv * a.nchunk, B, num_splits);
   switch (GH) {
-    case 1: return launch_scan_gh<1>(a, grid, stream);
-    case 2: return launch_scan_gh<2>(a, grid, stream);
-    case 4: return launch_scan_gh<4>(a, grid, stream);
-    default: return launch_scan_gh<8>(a, grid, stream);
+    case 1: return launch_scan_gh<1>(a, B, stream);
+    case 2: return launch_scan_gh<2>(a, B, stream);
+    case 4: return launch_scan_gh<4>(a, B, stream);
+    default: return launch_scan_gh<8>(a, B, stream);
   }
 }
 
@@ -396,6 +471,17 @@ extern "C" int gqa_decode_v2_launch(const uint16_t* q, const uint16_t* k_cache,
                                     int block_size, int max_blocks, float scale, int num_splits,
                                     float* ws_acc, float* ws_m, float* ws_l, hipStream_t stream) {
   if (B > 0 && !out) return hipErrorInvalidValue;
+  if (num_splits == 1) {
+    // One split: the single-pass kernel writes the output and the (one-split)
+    // workspace state itself; the merge would be an exact no-op.
+    hipError_t err = gqa::check_common(q, k_cache, v_cache, block_table, seq_lens, out, B, Hq, Hkv,
+                                       block_size, max_blocks);
+    if (err != hipSuccess) return err;
+    if (B > 0 && (!ws_acc || !ws_m || !ws_l)) return hipErrorInvalidValue;
+    if (B == 0) return hipSuccess;
+    return gqa::launch_scan(q, k_cache, v_cache, block_table, seq_lens, out, ws_acc, ws_m, ws_l,
+                            B, Hq, Hkv, block_size, max_blocks, scale, 1, stream);
+  }
   const int err = gqa_decode_v2_partial_launch(q, k_cache, v_cache, block_table, seq_lens, B, Hq,
                                                Hkv, block_size, max_blocks, scale, num_splits,
                                                ws_acc, ws_m, ws_l, stream);
@@ -408,16 +494,19 @@ extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
   return (size_t)B * Hq * num_splits * (gqa::kHeadDim + 2) * sizeof(float);
 }
 
-// Number of splits: enough (b, kv-head chunk, split) workgroups that every CU
-// holds kTargetWgsPerCu of them, but no more splits than keep each wave at
-// kMinTilesPerWave tiles of the longest request (shorter splits only add
-// workspace traffic and merge work). The longest request is bounded by
+// Number of splits. Two bounds, the larger wins:
+//  * fill: enough waves that every CU holds kTargetWavesPerCu of them (one per
+//    SIMD; two for 8-head groups, whose tiles cost twice the VALU work);
+//  * length: no split longer than kMaxChunk tokens, so one long request in a
+//    ragged batch cannot leave a tail of a few waves streaming alone.
+// and one cap: each wave keeps at least kMinTilesPerWave tiles (shorter splits
+// only add workspace traffic and merge work). The longest request is taken as
 // max_blocks * block_size, the only length the host knows without reading
 // seq_lens back from the device.
 extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size, int max_blocks,
                                           int num_cus) {
-  constexpr int kTargetWgsPerCu = 4;
-  constexpr int kMinTilesPerWave = 2;
+  constexpr int kMinTilesPerWave = 4;
+  constexpr int64_t kMaxChunk = 8192;
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || block_size < 1 || max_blocks < 1) return 0;
   if (num_cus <= 0) {
     int dev = 0;
@@ -427,14 +516,18 @@ extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size
       return 0;
   }
   const int G = Hq / Hkv;
-  const int GH = gqa::heads_per_wg(G);
-  const int64_t wgs1 = (int64_t)B * Hkv * ((G + GH - 1) / GH);
-  const int64_t target = (int64_t)num_cus * kTargetWgsPerCu;
-  int64_t ns = (target + wgs1 - 1) / wgs1;
+  const int GH = gqa::heads_per_wave(G);
+  const int P = gqa::waves_per_head(GH, 2);
+  const int waves_per_cu = GH == 8 ? 8 : 4;
+  const int64_t waves1 = (int64_t)B * Hkv * ((G + GH - 1) / GH) * P;
+  const int64_t target = (int64_t)num_cus * waves_per_cu;
   const int64_t s_max = (int64_t)max_blocks * block_size;
-  const int64_t min_chunk = (int64_t)gqa::kTile * gqa::kWaves * kMinTilesPerWave;
-  const int64_t ns_len = s_max / min_chunk > 1 ? s_max / min_chunk : 1;
-  if (ns > ns_len) ns = ns_len;
+  int64_t ns = (target + waves1 - 1) / waves1;
+  const int64_t ns_len = (s_max + kMaxChunk - 1) / kMaxChunk;
+  if (ns < ns_len) ns = ns_len;
+  const int64_t min_chunk = (int64_t)gqa::kTile * P * kMinTilesPerWave;
+  const int64_t ns_cap = s_max / min_chunk > 1 ? s_max / min_chunk : 1;
+  if (ns > ns_cap) ns = ns_cap;
   if (ns > GQA_DECODE_MAX_SPLITS) ns = GQA_DECODE_MAX_SPLITS;
   return ns < 1 ? 1 : (int)ns;
 }

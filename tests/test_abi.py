@@ -49,26 +49,40 @@ def test_workspace_bytes_invalid(args):
     assert capi.workspace_bytes(*args) == 0
 
 
-def test_pick_num_splits_properties():
-    cus = 256
-    # Representative shape: fills every CU, splits stay long.
-    ns = capi.pick_num_splits(32, 32, 8, 16, 512, cus)
+WAVES_PER_HEAD = 4     # waves sharing a kv-head (q-head groups up to 4)
+MIN_SPLIT_TOKENS = 4 * 16 * WAVES_PER_HEAD  # 4 tiles of 16 tokens per wave
+MAX_CHUNK = 8192
+
+
+@pytest.mark.parametrize("B,max_blocks,bs", [(1, 1, 16), (1, 8, 16), (1, 32, 16), (1, 512, 64),
+                                             (8, 512, 64), (32, 512, 16), (128, 2048, 16),
+                                             (4096, 64, 16), (2, 100000, 16)])
+def test_pick_num_splits_properties(B, max_blocks, bs):
+    cus, Hkv = 256, 8
+    s_max = max_blocks * bs
+    ns = capi.pick_num_splits(B, 32, Hkv, bs, max_blocks, cus)
     assert 1 <= ns <= 512
-    assert 32 * 8 * ns >= cus
-    assert math.ceil(8192 / ns) >= 128
-    # Fewer requests -> at least as many splits.
+    capped = ns == 512 or ns == max(1, s_max // MIN_SPLIT_TOKENS)
+    # Each split keeps the minimum length (or there is only one).
+    assert ns == 1 or s_max // ns >= MIN_SPLIT_TOKENS
+    if not capped:
+        # Enough waves for one per SIMD, and no split longer than MAX_CHUNK.
+        assert B * Hkv * WAVES_PER_HEAD * ns >= 4 * cus
+        assert math.ceil(s_max / ns) <= MAX_CHUNK
+        # And not more splits than either bound needs.
+        assert ns == 1 or (B * Hkv * WAVES_PER_HEAD * (ns - 1) < 4 * cus
+                           or math.ceil(s_max / (ns - 1)) > MAX_CHUNK)
+
+
+def test_pick_num_splits_headline_shapes():
+    # The representative shape fills the chip without splitting; fewer,
+    # longer requests split more.
+    assert capi.pick_num_splits(32, 32, 8, 16, 512, 256) == 1
     prev = 0
     for B in (128, 32, 8, 1):
-        cur = capi.pick_num_splits(B, 32, 8, 64, 512, cus)
+        cur = capi.pick_num_splits(B, 32, 8, 64, 512, 256)
         assert cur >= prev
         prev = cur
-    # Very short sequences are not split below the minimum split length.
-    assert capi.pick_num_splits(1, 32, 8, 16, 1, cus) == 1
-    assert capi.pick_num_splits(1, 32, 8, 16, 8, cus) == 1
-    # Never above the kernel's limit.
-    assert capi.pick_num_splits(1, 8, 8, 64, 1 << 20, 100000) == 512
-    # Enough work already: no split.
-    assert capi.pick_num_splits(4096, 32, 8, 16, 64, cus) == 1
 
 
 @pytest.mark.parametrize("args", [(0, 32, 8, 16, 512, 256), (32, 30, 8, 16, 512, 256),

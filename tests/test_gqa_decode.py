@@ -213,6 +213,26 @@ def test_capi_v2_matches_op(gpu):
     assert torch.equal(out1, gqa_decode_v1(*case, SCALE))
 
 
+def test_v2_one_split_writes_workspace(gpu):
+    """v2 with one split runs the single-pass kernel, which still fills the
+    caller's workspace with the one-split state."""
+    case = ref_case(CASES["a_base"])
+    q, k, v, bt, sl = case
+    B, Hq = q.shape[:2]
+    ws1, acc1, m1, l1 = alloc_ws(B, Hq, 1, q.device)
+    ws2, acc2, m2, l2 = alloc_ws(B, Hq, 1, q.device)
+    ws1.fill_(float("nan"))
+    out = torch.empty_like(q)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr())
+    assert capi.v2_launch(*args, out.data_ptr(), B, Hq, 8, 16, bt.shape[1], SCALE, 1,
+                          acc1.data_ptr(), m1.data_ptr(), l1.data_ptr(), stream_ptr()) == 0
+    assert capi.v2_partial_launch(*args, B, Hq, 8, 16, bt.shape[1], SCALE, 1, acc2.data_ptr(),
+                                  m2.data_ptr(), l2.data_ptr(), stream_ptr()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(ws1, ws2)
+    assert torch.equal(out, gqa_decode_v1(*case, SCALE))
+
+
 def test_current_stream_is_used(gpu):
     case = ref_case(CASES["a_base"])
     want = gqa_decode_v2(*case, SCALE, num_splits=4)
