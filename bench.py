@@ -8,7 +8,8 @@ input resident in HBM. The default workload is BASELINE.json config 2 (32Q/8KV,
 d=128, S=8192, B=32, block=16: 1 GiB of K+V), the shape the headline metric is
 quoted on; the other configs are selectable with --config.
 
-Timed region: W untimed steps, then K steps bracketed by
+Timed region: --ramp-seconds of untimed steps (steady clocks), W untimed
+steps, then K steps bracketed by
 torch.cuda.synchronize(). A v2 step is the C ABI's partial launch followed by
 its merge launch (one launch when num_splits is 1) on the current stream, with
 a caller-owned workspace. HIP events are recorded only between groups of steps
@@ -61,6 +62,8 @@ def parse_args(argv=None):
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="oracle threads (default: min(16, cpu count))")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--ramp-seconds", type=float, default=0.5,
+                    help="untimed steps before the warmup steps, to reach steady clocks")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="instead: time a plain device copy of MIB MiB (torch.neg into a second "
                          "buffer), the known-size kernel that calibrates rocprofv3's "
@@ -181,6 +184,14 @@ def main(argv=None):
             if rc != 0:
                 raise RuntimeError(f"launch failed: hipError_t {rc}")
 
+    # Clock ramp: the GPU takes a few hundred milliseconds of load to reach its
+    # steady clocks, far longer than W short steps; run untimed steps for
+    # --ramp-seconds first, then the W warmup steps.
+    t_ramp = time.perf_counter() + args.ramp_seconds
+    while time.perf_counter() < t_ramp:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

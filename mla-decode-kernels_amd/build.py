@@ -28,7 +28,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 KERNEL_LIB = os.path.join(LIB_DIR, "libgqa_decode_hip.so")
-HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip"]
+HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip", "gqa_decode_mfma.hip"]
 # Packed fp32 VALU ops are disabled for all device code.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
@@ -56,7 +56,8 @@ def build_kernels():
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
     tmp = KERNEL_LIB + ".tmp"
-    dt = _run([hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    extra = os.environ.get("GQA_HIPCC_FLAGS", "").split()  # experiments only
+    dt = _run([hipcc, *HIP_FLAGS, *extra, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
     os.replace(tmp, KERNEL_LIB)
     print(f"built {os.path.relpath(KERNEL_LIB, REPO_ROOT)} in {dt:.1f}s")
     return KERNEL_LIB

@@ -19,20 +19,23 @@
 //
 // Split rule: segment `split` of request b covers
 // [split*chunk, min(S, (split+1)*chunk)) with chunk = ceil(S/num_splits)
-// rounded up to a multiple of 16 tokens (v2_splitkv.cu:30-32 without the
-// rounding). The rounding keeps every tile inside one cache block whenever
-// block_size is a multiple of 16, which lets the block id be a scalar load.
+// rounded up to a multiple of 32 tokens (v2_splitkv.cu:30-32 without the
+// rounding). The rounding keeps every 16-token group inside one cache block
+// whenever block_size is a multiple of 16, which lets the block id be a scalar
+// load, and is the same for both scan kernels.
 // Splits past the end of a short request are empty and store the neutral
 // state (-inf, 0, 0), whose merge factor is 0 (v2_splitkv.cu:33-40).
 // num_splits == 1 runs the single-pass kernel, so v2 with one split equals v1
 // bit for bit.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
+#include "gqa_scan.hpp"
 #include "gqa_decode.h"
 
 namespace gqa {
 
 constexpr int kTile = 16;   // tokens per wave per tile
+constexpr int kChunkAlign = 32;  // split lengths are multiples of this (both scan kernels)
 constexpr int kLoads = 4;   // 16-byte K loads (and V loads) per lane per tile
 
 // Launch shapes. A workgroup holds P waves that share one kv-head of one
@@ -41,29 +44,17 @@ constexpr int kLoads = 4;   // 16-byte K loads (and V loads) per lane per tile
 // one wave per SIMD resident (4 per CU), each keeping one tile in flight while
 // it consumes the previous one; more resident waves or deeper prefetch only add
 // queueing. P = 4 waves per kv-head keeps a workgroup's reads adjacent and the
-// merge in LDS; 8-head groups (GH = 8) run P = 1 to stay within 256 VGPRs at
-// two waves per SIMD, which their larger VALU share needs.
-constexpr int kWavesPerHead = 4;      // P for GH <= 4 (and every single-pass launch)
-constexpr int kWavesPerHeadGH8 = 1;   // P for GH = 8 split launches
-constexpr int kScanDepth = 2;         // register tiles in flight per wave
-inline int waves_per_head(int GH, int num_splits) {
-  return (GH == 8 && num_splits > 1) ? kWavesPerHeadGH8 : kWavesPerHead;
-}
+// merge in LDS.
+// GQA groups larger than this run the matrix-core scan (gqa_decode_mfma.hip):
+// its VALU work per tile does not grow with the group, while this kernel's
+// does (measured: 8-head groups are VALU-bound here at ~60% of HBM peak and
+// reach ~72% on MFMA; 4-head groups stream ~5% faster here).
+#ifndef GQA_MFMA_MIN_GROUP
+#define GQA_MFMA_MIN_GROUP 5
+#endif
+constexpr int kWavesPerHead = 4;  // P: waves sharing a kv-head (both kernels)
+constexpr int kScanDepth = 2;     // register tiles in flight per wave
 
-struct ScanArgs {
-  const uint16_t* q;
-  const uint16_t* k_cache;
-  const uint16_t* v_cache;
-  const int* block_table;
-  const int* seq_lens;
-  uint16_t* out;  // single-pass mode: normalised bf16 output (num_splits == 1)
-  float* ws_acc;  // split mode: unnormalised per-split state
-  float* ws_m;
-  float* ws_l;
-  int Hq, Hkv, G, nchunk, block_size, max_blocks, num_splits;
-  FastDiv bs_div;
-  float scale_log2e;  // scale * log2(e): scores are kept in base-2 units
-};
 
 struct TileRegs {
   uint4 k[kLoads];
@@ -89,7 +80,7 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs 
 
   const int S = max(a.seq_lens[b], 0);
   const int ns = a.num_splits;
-  const int chunk = ((S + ns - 1) / ns + (kTile - 1)) & ~(kTile - 1);
+  const int chunk = ((S + ns - 1) / ns + (kChunkAlign - 1)) & ~(kChunkAlign - 1);
   const int seg_start = min(split * chunk, S);
   const int seg_end = min(S, seg_start + chunk);
   const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
@@ -365,10 +356,10 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(const float* __re
   reinterpret_cast<uint32_t*>(out + (size_t)bh * kHeadDim)[lane] = lo | (hi << 16);
 }
 
-// q-heads served per wave: the whole group up to 8, rounded up to a power of
-// two (extra heads carry q = 0 and are not written); larger groups are cut into
-// chunks of 8 that each scan the same K/V.
-inline int heads_per_wave(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8; }
+// q-heads served per wave of this kernel: the whole group (at most 4 here),
+// rounded up to a power of two; extra heads carry q = 0 and are not written.
+inline int heads_per_wave(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : 4; }
+inline bool use_mfma(int G) { return G >= GQA_MFMA_MIN_GROUP; }
 
 template <int GH, int P>
 hipError_t launch_scan_shape(const ScanArgs& a, dim3 grid, hipStream_t stream) {
@@ -384,7 +375,6 @@ hipError_t launch_scan_shape(const ScanArgs& a, dim3 grid, hipStream_t stream) {
 template <int GH>
 hipError_t launch_scan_gh(const ScanArgs& a, int B, hipStream_t stream) {
   const dim3 grid(a.Hkv * a.nchunk, B, a.num_splits);
-  if (waves_per_head(GH, a.num_splits) == 1) return launch_scan_shape<GH, 1>(a, grid, stream);
   return launch_scan_shape<GH, kWavesPerHead>(a, grid, stream);
 }
 
@@ -412,11 +402,11 @@ hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_
   a.num_splits = num_splits;
   a.bs_div = make_fastdiv((uint32_t)block_size);
   a.scale_log2e = (float)((double)scale * 1.4426950408889634);
+  if (use_mfma(a.G)) return launch_scan_mfma(a, B, stream);
   switch (GH) {
     case 1: return launch_scan_gh<1>(a, B, stream);
     case 2: return launch_scan_gh<2>(a, B, stream);
-    case 4: return launch_scan_gh<4>(a, B, stream);
-    default: return launch_scan_gh<8>(a, B, stream);
+    default: return launch_scan_gh<4>(a, B, stream);
   }
 }
 
@@ -495,8 +485,9 @@ extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
 }
 
 // Number of splits. Two bounds, the larger wins:
-//  * fill: enough waves that every CU holds kTargetWavesPerCu of them (one per
-//    SIMD; two for 8-head groups, whose tiles cost twice the VALU work);
+//  * fill: enough waves that every CU holds 4 of them (one per SIMD; 8 for the
+//    matrix-core scan, whose longer per-tile dependency chain needs a second
+//    wave per SIMD to hide);
 //  * length: no split longer than kMaxChunk tokens, so one long request in a
 //    ragged batch cannot leave a tail of a few waves streaming alone.
 // and one cap: each wave keeps at least kMinTilesPerWave tiles (shorter splits
@@ -516,9 +507,10 @@ extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size
       return 0;
   }
   const int G = Hq / Hkv;
-  const int GH = gqa::heads_per_wave(G);
-  const int P = gqa::waves_per_head(GH, 2);
-  const int waves_per_cu = GH == 8 ? 8 : 4;
+  const bool mfma = gqa::use_mfma(G);
+  const int GH = mfma ? 16 : gqa::heads_per_wave(G);  // q-heads per wave
+  const int P = gqa::kWavesPerHead;
+  const int waves_per_cu = mfma ? 8 : 4;
   const int64_t waves1 = (int64_t)B * Hkv * ((G + GH - 1) / GH) * P;
   const int64_t target = (int64_t)num_cus * waves_per_cu;
   const int64_t s_max = (int64_t)max_blocks * block_size;

@@ -124,9 +124,9 @@ def test_group_sizes(gpu, Hq, Hkv):
         run_and_check(fn, case, want=want, label=f"{kernel}/G{Hq // Hkv}")
 
 
-def build_segments(S, ns, tile=16):
+def build_segments(S, ns, tile=32):
     """The partial kernel's documented segment rule: chunk = ceil(S/ns)
-    rounded up to a multiple of 16 tokens."""
+    rounded up to a multiple of 32 tokens."""
     chunk = -(-(-(-S // ns)) // tile) * tile
     return [(min(i * chunk, S), min(S, min(i * chunk, S) + chunk)) for i in range(ns)]
 
@@ -141,6 +141,12 @@ def alloc_ws(B, Hq, ns, device):
 
 def stream_ptr():
     return torch.cuda.current_stream().cuda_stream
+
+
+# The matrix-core scan rounds the softmax weights to bf16 before the PV product
+# (and sums the same rounded weights into l), so a state's l and acc may differ
+# from the exact ones by up to 2^-9 relative per weight.
+W_REL = 2.5e-3
 
 
 @pytest.mark.parametrize("ns", [1, 4, 9])
@@ -171,8 +177,10 @@ def test_partial_states_match_oracle(gpu, ns):
                     assert not acc_h[b, h, i].any()
                     continue
                 assert m_h[b, h, i] == pytest.approx(mw, abs=1e-5)
-                assert l_h[b, h, i] == pytest.approx(lw, rel=1e-4)
-                np.testing.assert_allclose(acc_h[b, h, i], aw, rtol=1e-3, atol=1e-4)
+                assert l_h[b, h, i] == pytest.approx(lw, rel=W_REL)
+                # |acc error| <= W_REL * sum_t p_t |v_t| <= W_REL * l * max|v|
+                vmax = float(np.abs(V[a:e, h // 4]).max())
+                np.testing.assert_allclose(acc_h[b, h, i], aw, rtol=0, atol=W_REL * lw * vmax)
 
 
 def test_merge_entry_point(gpu):
