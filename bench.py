@@ -85,6 +85,14 @@ def read_traffic(config, kernel, num_splits):
     return None
 
 
+def kernel_name(kernel, group):
+    """The dominant kernel of one step: v0's kernel, else the scan kernel the
+    dispatcher picks for this GQA group size (matrix cores from 5 q-heads)."""
+    if kernel == "v0":
+        return "gqa_decode_v0_kernel"
+    return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
+
+
 def gpu_clocks():
     """Current shader and memory clocks from the amdgpu sysfs DPM tables (the
     entry marked '*'); read directly so no helper process is started."""
@@ -272,8 +280,8 @@ def main(argv=None):
         "kv_bytes": kvb,
         "sol_us": round(sol, 3),
         "op_median_us": round(op_ms * 1e3, 3),
-        "roofline": {"bound": "hbm", "kernel": "gqa_decode_scan_kernel" if args.kernel != "v0"
-                     else "gqa_decode_v0_kernel", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv),
+                     "achieved": round(achieved, 1),
                      "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
                      "avg_kernel_us": round(kern_avg_us, 3),
                      "traffic": traffic},
