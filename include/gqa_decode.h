@@ -109,11 +109,12 @@ GQA_DECODE_API int gqa_decode_v2_merge_launch(const float* ws_acc, const float* 
  * workspace inline at python/gqa_decode_ext.cpp:106-109). */
 GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits);
 
-/* Split count that fills the device: enough (b, kv-head, split) workgroups
- * for every CU, while keeping each split long enough that the workspace
- * round trip stays small next to the KV stream. max_blocks*block_size is
- * taken as the longest sequence. num_cus <= 0 means "query the current
- * device". Returns a value in [1, GQA_DECODE_MAX_SPLITS], or 0 for invalid
+/* Split count that fills the device: as many (b, kv-head, split) waves as
+ * fit one round of one wave per SIMD (two for the matrix-core scan on
+ * sequences of 8192+ tokens), no split longer than 8192 tokens, each wave
+ * keeping at least two 16-token tiles, and at most 32 splits.
+ * max_blocks*block_size is taken as the longest sequence. num_cus <= 0 means
+ * "query the current device". Returns a value in [1, 32], or 0 for invalid
  * arguments. No reference counterpart: the reference defaults to 8
  * (python/gqa_decode_ext.cpp:133) and picks the best value by sweep
  * (bench/run_matrix.py:84-94). Pure host code. */

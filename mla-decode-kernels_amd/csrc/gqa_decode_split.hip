@@ -485,19 +485,25 @@ extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
 }
 
 // Number of splits. Two bounds, the larger wins:
-//  * fill: enough waves that every CU holds 4 of them (one per SIMD; 8 for the
-//    matrix-core scan, whose longer per-tile dependency chain needs a second
-//    wave per SIMD to hide);
+//  * fill: as many waves as fit in one round of the target residency -- one
+//    wave per SIMD (4 per CU), or two for the matrix-core scan on long
+//    sequences, whose per-tile dependency chain needs a second wave per SIMD
+//    to hide -- rounded down: a round that is even slightly over-full leaves
+//    its excess waves to run alone afterwards (measured: 8 requests of 32768
+//    tokens take 182 us at 1024 waves, 246 us at 1280);
 //  * length: no split longer than kMaxChunk tokens, so one long request in a
-//    ragged batch cannot leave a tail of a few waves streaming alone.
-// and one cap: each wave keeps at least kMinTilesPerWave tiles (shorter splits
-// only add workspace traffic and merge work). The longest request is taken as
-// max_blocks * block_size, the only length the host knows without reading
-// seq_lens back from the device.
+//    ragged batch cannot leave a tail of a few waves streaming alone;
+// and two caps: each wave keeps at least kMinTilesPerWave tiles, and at most
+// kMaxSplits splits (the merge walks the splits of a head in order, so very
+// many short splits cost more to merge than they gain). The longest request
+// is taken as max_blocks * block_size, the only length the host knows without
+// reading seq_lens back from the device.
 extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size, int max_blocks,
                                           int num_cus) {
-  constexpr int kMinTilesPerWave = 4;
+  constexpr int kMinTilesPerWave = 2;
   constexpr int64_t kMaxChunk = 8192;
+  constexpr int64_t kLongSequence = 8192;
+  constexpr int64_t kMaxSplits = 32;
   if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv != 0 || block_size < 1 || max_blocks < 1) return 0;
   if (num_cus <= 0) {
     int dev = 0;
@@ -510,16 +516,16 @@ extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size
   const bool mfma = gqa::use_mfma(G);
   const int GH = mfma ? 16 : gqa::heads_per_wave(G);  // q-heads per wave
   const int P = gqa::kWavesPerHead;
-  const int waves_per_cu = mfma ? 8 : 4;
+  const int64_t s_max = (int64_t)max_blocks * block_size;
+  const int waves_per_cu = (mfma && s_max >= kLongSequence) ? 8 : 4;
   const int64_t waves1 = (int64_t)B * Hkv * ((G + GH - 1) / GH) * P;
   const int64_t target = (int64_t)num_cus * waves_per_cu;
-  const int64_t s_max = (int64_t)max_blocks * block_size;
-  int64_t ns = (target + waves1 - 1) / waves1;
+  int64_t ns = target / waves1;
   const int64_t ns_len = (s_max + kMaxChunk - 1) / kMaxChunk;
   if (ns < ns_len) ns = ns_len;
   const int64_t min_chunk = (int64_t)gqa::kTile * P * kMinTilesPerWave;
   const int64_t ns_cap = s_max / min_chunk > 1 ? s_max / min_chunk : 1;
   if (ns > ns_cap) ns = ns_cap;
-  if (ns > GQA_DECODE_MAX_SPLITS) ns = GQA_DECODE_MAX_SPLITS;
+  if (ns > kMaxSplits) ns = kMaxSplits;
   return ns < 1 ? 1 : (int)ns;
 }

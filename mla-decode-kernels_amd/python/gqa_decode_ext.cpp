@@ -6,11 +6,14 @@
 // allocated from the caching allocator (:69, :105-109), launch on the current
 // stream (:70, :110). Additions: a device guard, num_splits == 0 selecting the
 // split-count heuristic (widening the accepted domain [1, 512] of :102-103),
-// a check of the launcher's return code, and one workspace allocation carved
-// into the three arrays instead of three.
+// a check of the launcher's return code, one workspace allocation carved
+// into the three arrays instead of three, and none at all for one split (the
+// single-pass kernel runs instead, with bitwise the same output).
 //
 // This file is host-only C++ (compiled by g++); all device code lives in the
 // hipcc-built libgqa_decode_hip.so it links against.
+#include <atomic>
+
 #include <torch/extension.h>
 
 #include <c10/core/DeviceGuard.h>
@@ -107,10 +110,16 @@ torch::Tensor gqa_decode_v1(torch::Tensor q, torch::Tensor k_cache, torch::Tenso
 }
 
 int64_t pick_num_splits(const GqaDims& d, const torch::Tensor& q) {
-  int cus = 0;
+  // CU count per device, queried once (a racing first query stores the same value).
+  static std::atomic<int> cu_count[64];
   const int dev = q.device().index();
-  TORCH_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess,
-              "could not query the CU count of device ", dev);
+  int cus = dev >= 0 && dev < 64 ? cu_count[dev].load(std::memory_order_relaxed) : 0;
+  if (cus <= 0) {
+    TORCH_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ==
+                    hipSuccess && cus > 0,
+                "could not query the CU count of device ", dev);
+    if (dev >= 0 && dev < 64) cu_count[dev].store(cus, std::memory_order_relaxed);
+  }
   return gqa_decode_pick_num_splits((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
                                     (int)d.max_blocks, cus);
 }
@@ -125,6 +134,13 @@ torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tenso
   if (num_splits == 0) num_splits = d.B > 0 ? pick_num_splits(d, q) : 1;
   TORCH_CHECK(num_splits >= 1, "num_splits heuristic failed");
 
+  if (num_splits == 1) {
+    // The op never hands its workspace back, and one split gives output
+    // bitwise equal to the single-pass kernel's (a guarantee of the C ABI),
+    // so it launches that kernel and allocates no workspace.
+    return gqa_decode_run(gqa_decode_v1_launch, "gqa_decode_v1_launch", q, k_cache, v_cache,
+                          block_table, seq_lens, scale);
+  }
   auto out = torch::empty_like(q);
   auto f32 = torch::TensorOptions().dtype(torch::kFloat32).device(q.device());
   const int64_t states = d.B * d.Hq * num_splits;

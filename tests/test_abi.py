@@ -49,35 +49,55 @@ def test_workspace_bytes_invalid(args):
     assert capi.workspace_bytes(*args) == 0
 
 
-WAVES_PER_HEAD = 4     # waves sharing a kv-head (q-head groups up to 4)
-MIN_SPLIT_TOKENS = 4 * 16 * WAVES_PER_HEAD  # 4 tiles of 16 tokens per wave
+WAVES_PER_HEAD = 4     # waves sharing a kv-head
+MIN_SPLIT_TOKENS = 2 * 16 * WAVES_PER_HEAD  # two 16-token tiles per wave
 MAX_CHUNK = 8192
+MAX_SPLITS = 32
 
 
+def waves_per_split(B, Hq, Hkv):
+    G = Hq // Hkv
+    per_wave = 16 if G >= 5 else (1 if G <= 1 else 2 if G <= 2 else 4)
+    return B * Hkv * -(-G // per_wave) * WAVES_PER_HEAD
+
+
+def target_waves(Hq, Hkv, s_max, cus):
+    mfma = Hq // Hkv >= 5
+    return cus * (8 if mfma and s_max >= 8192 else 4)
+
+
+@pytest.mark.parametrize("Hq", [32, 64])
 @pytest.mark.parametrize("B,max_blocks,bs", [(1, 1, 16), (1, 8, 16), (1, 32, 16), (1, 512, 64),
-                                             (8, 512, 64), (32, 512, 16), (128, 2048, 16),
-                                             (4096, 64, 16), (2, 100000, 16)])
-def test_pick_num_splits_properties(B, max_blocks, bs):
+                                             (3, 512, 16), (8, 512, 64), (32, 512, 16),
+                                             (128, 2048, 16), (4096, 64, 16), (2, 100000, 16)])
+def test_pick_num_splits_properties(B, max_blocks, bs, Hq):
     cus, Hkv = 256, 8
     s_max = max_blocks * bs
-    ns = capi.pick_num_splits(B, 32, Hkv, bs, max_blocks, cus)
-    assert 1 <= ns <= 512
-    capped = ns == 512 or ns == max(1, s_max // MIN_SPLIT_TOKENS)
-    # Each split keeps the minimum length (or there is only one).
-    assert ns == 1 or s_max // ns >= MIN_SPLIT_TOKENS
-    if not capped:
-        # Enough waves for one per SIMD, and no split longer than MAX_CHUNK.
-        assert B * Hkv * WAVES_PER_HEAD * ns >= 4 * cus
-        assert math.ceil(s_max / ns) <= MAX_CHUNK
-        # And not more splits than either bound needs.
-        assert ns == 1 or (B * Hkv * WAVES_PER_HEAD * (ns - 1) < 4 * cus
-                           or math.ceil(s_max / (ns - 1)) > MAX_CHUNK)
+    ns = capi.pick_num_splits(B, Hq, Hkv, bs, max_blocks, cus)
+    per = waves_per_split(B, Hq, Hkv)
+    target = target_waves(Hq, Hkv, s_max, cus)
+    cap = min(MAX_SPLITS, max(1, s_max // MIN_SPLIT_TOKENS))
+    assert 1 <= ns <= cap
+    length = -(-s_max // MAX_CHUNK)
+    if ns < cap:
+        # No split longer than MAX_CHUNK ...
+        assert -(-s_max // ns) <= MAX_CHUNK
+        # ... and the fill bound is maximal: one more split would overfill
+        # the round of resident waves.
+        assert (ns + 1) * per > target
+    if ns > 1 and ns > length:
+        # Splits beyond the length bound only fill the round, never overfill it.
+        assert ns * per <= target
 
 
 def test_pick_num_splits_headline_shapes():
-    # The representative shape fills the chip without splitting; fewer,
-    # longer requests split more.
+    # BASELINE configs 1..5 on 256 CUs: the representative shape fills the
+    # chip without splitting; fewer, longer requests split more.
+    assert capi.pick_num_splits(1, 32, 8, 16, 32, 256) == 4
     assert capi.pick_num_splits(32, 32, 8, 16, 512, 256) == 1
+    assert capi.pick_num_splits(8, 32, 8, 64, 512, 256) == 4
+    assert capi.pick_num_splits(32, 64, 8, 64, 512, 256) == 4
+    assert capi.pick_num_splits(128, 32, 8, 16, 2048, 256) == 4
     prev = 0
     for B in (128, 32, 8, 1):
         cur = capi.pick_num_splits(B, 32, 8, 64, 512, 256)
