@@ -93,26 +93,6 @@ def kernel_name(kernel, group):
     return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
 
 
-def gpu_clocks():
-    """Current shader and memory clocks from the amdgpu sysfs DPM tables (the
-    entry marked '*'); read directly so no helper process is started."""
-    import glob
-
-    out = {}
-    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
-        for key, fname in (("sclk", "pp_dpm_sclk"), ("mclk", "pp_dpm_mclk")):
-            try:
-                with open(os.path.join(dev, fname)) as f:
-                    cur = [ln.split(":", 1)[1].strip(" *\n") for ln in f if ln.rstrip().endswith("*")]
-                if cur:
-                    out.setdefault(key, cur[0])
-            except OSError:
-                pass
-        if out:
-            break
-    return out or "unavailable"
-
-
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -286,7 +266,7 @@ def main(argv=None):
                      "avg_kernel_us": round(kern_avg_us, 3),
                      "traffic": traffic},
         "device": props.name, "gcn_arch": props.gcnArchName, "cus": props.multi_processor_count,
-        "clocks": gpu_clocks(),
+        "clocks": cases.gpu_clocks(),
     }
     if sweep:
         result["sweep_us"] = sweep

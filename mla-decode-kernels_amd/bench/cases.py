@@ -166,3 +166,78 @@ def host_case(case, batches=None):
         off += n[i]
     return (bits(q[batches]), bits(k.index_select(0, idx)), bits(v.index_select(0, idx)),
             new_bt, sl_h.astype(np.int32))
+
+
+def gpu_clocks():
+    """Current shader and memory clocks from the amdgpu sysfs DPM tables (the
+    entry marked '*'); read directly so no helper process is started."""
+    import glob
+    import os
+
+    out = {}
+    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
+        for key, fname in (("sclk", "pp_dpm_sclk"), ("mclk", "pp_dpm_mclk")):
+            try:
+                with open(os.path.join(dev, fname)) as f:
+                    cur = [ln.split(":", 1)[1].strip(" *\n") for ln in f if ln.rstrip().endswith("*")]
+                if cur:
+                    out.setdefault(key, cur[0])
+            except OSError:
+                pass
+        if out:
+            break
+    return out or "unavailable"
+
+
+def torch_ref_fp32(q, k_cache, v_cache, block_table, seq_lens, scale, batches):
+    """fp32 GQA decode of the listed requests, in torch on the tensors' device:
+    gather the request's pages, fp32 scores, softmax, weighted V sum. A spot
+    check for benchmark runs (the test suite checks against the CPU oracle)."""
+    bs, Hkv, Dh = k_cache.shape[1:]
+    Hq = q.shape[1]
+    G = Hq // Hkv
+    lens = seq_lens.tolist()
+    outs = []
+    for b in batches:
+        S = int(lens[b])
+        n = (S + bs - 1) // bs
+        ids = block_table[b, :n].long()
+        k = k_cache.index_select(0, ids).view(n * bs, Hkv, Dh)[:S].float()
+        v = v_cache.index_select(0, ids).view(n * bs, Hkv, Dh)[:S].float()
+        k = k.permute(1, 2, 0).contiguous()                 # [Hkv, D, S]
+        v = v.permute(1, 0, 2).contiguous()                 # [Hkv, S, D]
+        qb = q[b].float().view(Hkv, G, Dh)
+        p = torch.softmax(torch.bmm(qb, k) * scale, dim=-1)  # [Hkv, G, S]
+        outs.append(torch.bmm(p, v).reshape(Hq, Dh))
+    return torch.stack(outs)
+
+
+def spot_check(fn, case, scale, label="kernel", nb=2, tol=2e-2):
+    """Run fn(*case, scale) once and compare its first min(nb, B) requests with
+    torch_ref_fp32 (bench/common.py:75-89 of the reference). Returns the
+    max-abs error; raises AssertionError beyond atol = rtol = tol."""
+    nb = min(nb, case[0].shape[0])
+    out = fn(*case, scale)
+    torch.cuda.synchronize()
+    ref = torch_ref_fp32(*case, scale, range(nb))
+    got = out[:nb].float()
+    max_abs = (got - ref).abs().max().item()
+    assert torch.allclose(got, ref, atol=tol, rtol=tol), (
+        f"{label} spot check failed on first {nb} requests: max-abs={max_abs:.4e}")
+    return max_abs
+
+
+def time_ops_two_pass(fns, warmup=10, runs=50):
+    """Median time in milliseconds of each zero-argument callable in `fns`
+    (name -> fn), each measured as time_op measures it (the reference's
+    method: back-to-back calls, events around each, synchronize after each),
+    in two passes over the callables, the second in reverse order; each keeps
+    the lower of its two medians. Slow drifts within a run (clocks, power
+    state) then cannot favour whichever callable happens to be measured last."""
+    names = list(fns)
+    best = {}
+    for order in (names, names[::-1]):
+        for name in order:
+            t = time_op(fns[name], warmup, runs)
+            best[name] = min(best.get(name, t), t)
+    return best

@@ -1,0 +1,227 @@
+"""64-cell benchmark matrix on MI355X: the gfx950 kernels beside a library
+baseline, cell by cell comparable with the reference's H100 matrix.
+
+Counterpart of the reference's bench/run_matrix.py:34-175. Grid: headtype
+{(32,8),(64,8)} x S {512,2048,8192,32768} x B {1,8,32,128} x block {16,64}.
+Per cell (uniform lengths, q/k/v = 0.5 * N(0,1) bf16 from seed 0, shuffled
+pool of 1.1x the needed blocks):
+
+* spot check of v1 and of the baseline on the first two requests against an
+  fp32 torch reference (atol = rtol = 2e-2);
+* median time (HIP events around each call, bench/common.py:49-64 of the
+  reference) of the baseline's run() only, v1, v2 at num_splits
+  {1,4,8,16,32,64} (best recorded) and at the split heuristic (num_splits=0),
+  and v0 where it is not prohibitively slow (S <= 2048 and B <= 8);
+* 0.5 s of untimed calls (steady clocks), then each variant timed as the
+  reference times it -- 10 warmup calls, 50 timed (30 for S=32768, B>=32),
+  events around each call, synchronize after each -- in two passes over the
+  variants, the second in reverse order, keeping each variant's lower
+  median, so that clock drift within the cell does not favour whichever
+  variant is measured last. (Cells of a few microseconds sit on the launch
+  and power-state floor; their times carry no bandwidth information.)
+
+The baseline is torch SDPA on AOTriton over pages gathered into contiguous
+K/V at plan time (baselines/sdpa_adapter.py); with --baseline none it is
+skipped. Each cell writes its own JSON into --out-dir and is skipped when that
+file exists, so an interrupted run resumes; matrix_summary.csv is rebuilt
+from all cell files at the end.
+"""
+
+import argparse
+import csv
+import itertools
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, _HERE)
+sys.path.insert(0, os.path.join(os.path.dirname(_HERE), "python"))
+
+import cases  # noqa: E402
+from binding import KERNELS, gqa_decode_v2, num_splits_heuristic  # noqa: E402
+
+HEADTYPES = [(32, 8), (64, 8)]
+S_LIST = [512, 2048, 8192, 32768]
+B_LIST = [1, 8, 32, 128]
+BLOCK_LIST = [16, 64]
+SPLITS_LIST = [1, 4, 8, 16, 32, 64]
+POOL_FACTOR = 1.1
+MEM_LIMIT_GIB = 200.0
+RAMP_SECONDS = 0.5
+
+
+def cell_name(Hq, Hkv, S, B, bs):
+    return f"cell_{Hq}x{Hkv}_S{S}_B{B}_bs{bs}"
+
+
+def all_cells():
+    return [(Hq, Hkv, S, B, bs) for (Hq, Hkv), S, B, bs
+            in itertools.product(HEADTYPES, S_LIST, B_LIST, BLOCK_LIST)]
+
+
+def memory_precheck(cells, baseline):
+    """Refuse to start if the largest cell (pool, plus the baseline's
+    contiguous copy) cannot fit."""
+    need = max(cases.kv_bytes([S] * B, Hkv) * (POOL_FACTOR + (1 if baseline else 0))
+               for _, Hkv, S, B, _ in cells) / 2**30
+    total = torch.cuda.get_device_properties(0).total_memory / 2**30
+    print(f"memory precheck: largest cell needs ~{need:.1f} GiB, device {total:.1f} GiB",
+          flush=True)
+    if need > min(MEM_LIMIT_GIB, 0.8 * total):
+        raise SystemExit(f"largest cell needs {need:.1f} GiB, over the limit")
+
+
+def ramp(fn, seconds):
+    t_end = time.time() + seconds
+    while time.time() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def make_baseline(name, case, scale):
+    if name == "sdpa":
+        from baselines.sdpa_adapter import make_sdpa_runner
+        return make_sdpa_runner(*case, scale)
+    raise ValueError(f"unknown baseline {name!r}")
+
+
+def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
+    scale = 1.0 / math.sqrt(cases.D)
+    case = cases.make_case([S] * B, Hq, Hkv, bs, pool_factor=POOL_FACTOR, seed=0, qkv_std=0.5)
+    kvb = cases.kv_bytes([S] * B, Hkv)
+    sol_ms = cases.sol_us(kvb) / 1e3
+    checks = {"v1": cases.spot_check(KERNELS["v1"], case, scale, label="v1")}
+
+    warmup, runs = (10, 30) if (S == 32768 and B >= 32) else (10, 50)
+    h = num_splits_heuristic(B, Hq, Hkv, bs, case[3].shape[1], num_cus)
+    checks["v2_heuristic"] = cases.spot_check(
+        lambda *a: gqa_decode_v2(*a, num_splits=0), case, scale, label="v2 heuristic")
+
+    fns = {}
+    if baseline != "none":
+        run = make_baseline(baseline, case, scale)
+        checks[baseline] = cases.spot_check(lambda *a: run(), case, scale, label=baseline)
+        fns[baseline] = run
+    fns["v1"] = lambda: KERNELS["v1"](*case, scale)
+    for ns in SPLITS_LIST:
+        fns[f"v2/{ns}"] = (lambda n: lambda: gqa_decode_v2(*case, scale, num_splits=n))(ns)
+    fns["v2_heuristic"] = lambda: gqa_decode_v2(*case, scale, num_splits=0)
+    if S <= 2048 and B <= 8:
+        fns["v0"] = lambda: KERNELS["v0"](*case, scale)
+
+    # Clocks drop while the host builds the case; bring them back up first.
+    ramp(fns["v2_heuristic"], RAMP_SECONDS)
+    ms = cases.time_ops_two_pass(fns, warmup, runs)
+
+    def entry(t, **extra):
+        return dict(median_ms=t, pct_of_sol=sol_ms / t * 100, **extra)
+
+    results = {}
+    if baseline != "none":
+        results[baseline] = entry(ms[baseline])
+    results["v1"] = entry(ms["v1"])
+    by_splits = {ns: ms[f"v2/{ns}"] for ns in SPLITS_LIST}
+    best = min(by_splits, key=by_splits.get)
+    results["v2"] = entry(by_splits[best], by_splits=by_splits, best_splits=best)
+    results["v2_heuristic"] = entry(ms["v2_heuristic"], num_splits=h)
+    if "v0" in ms:
+        results["v0"] = entry(ms["v0"])
+
+    return {
+        "Hq": Hq, "Hkv": Hkv, "S": S, "B": B, "block": bs,
+        "warmup": warmup, "runs": runs, "pool_factor": POOL_FACTOR,
+        "timing": "events around each call, sync after each; two passes, lower median",
+        "kv_bytes": kvb, "sol_ms": sol_ms, "peak_bytes_per_s": cases.HBM_PEAK_BYTES_PER_S,
+        "spot_check": {k: f"passed (max-abs {v:.3e})" for k, v in checks.items()},
+        "baseline": baseline,
+        "clocks": cases.gpu_clocks(),
+        "results": results,
+    }
+
+
+def write_summary(out_dir):
+    rows = []
+    for fname in sorted(os.listdir(out_dir)):
+        if not (fname.startswith("cell_") and fname.endswith(".json")):
+            continue
+        with open(os.path.join(out_dir, fname)) as f:
+            cell = json.load(f)
+        base = cell["results"].get(cell.get("baseline", ""), {}).get("median_ms")
+        for kernel, r in cell["results"].items():
+            rows.append({
+                "headtype": f"{cell['Hq']}x{cell['Hkv']}",
+                "S": cell["S"], "B": cell["B"], "block": cell["block"],
+                "kernel": kernel,
+                "num_splits": r.get("best_splits", r.get("num_splits", "")),
+                "median_ms": r["median_ms"],
+                "pct_of_sol": r["pct_of_sol"],
+                # > 1: faster than the baseline
+                "ratio_vs_baseline": base / r["median_ms"] if base else "",
+            })
+    if not rows:
+        return
+    path = os.path.join(out_dir, "matrix_summary.csv")
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+        w.writeheader()
+        w.writerows(rows)
+    print(f"wrote {path} ({len(rows)} rows)", flush=True)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--out-dir", default=None,
+                    help="matrix directory (resumed if it exists); default results/matrix_<ts>")
+    ap.add_argument("--baseline", default="sdpa", choices=["sdpa", "none"])
+    ap.add_argument("--only", default=None,
+                    help="comma-separated substrings; run only cells whose name contains one")
+    args = ap.parse_args(argv)
+
+    out_dir = args.out_dir or os.path.join(_HERE, "results",
+                                           time.strftime("matrix_%Y%m%d_%H%M%S"))
+    os.makedirs(out_dir, exist_ok=True)
+    print(f"matrix output dir: {out_dir}", flush=True)
+
+    cells = all_cells()
+    if args.only:
+        keys = args.only.split(",")
+        cells = [c for c in cells if any(k in cell_name(*c) for k in keys)]
+    memory_precheck(cells, args.baseline != "none")
+    num_cus = torch.cuda.get_device_properties(0).multi_processor_count
+
+    durations = []
+    for i, c in enumerate(cells, 1):
+        name = cell_name(*c)
+        path = os.path.join(out_dir, f"{name}.json")
+        if os.path.exists(path):
+            print(f"[{i}/{len(cells)}] {name}: exists, skipping", flush=True)
+            continue
+        print(f"[{i}/{len(cells)}] {name}: running", flush=True)
+        t0 = time.time()
+        cell = run_cell(*c, args.baseline, num_cus)
+        with open(path, "w") as f:
+            json.dump(cell, f, indent=2)
+        torch.cuda.empty_cache()
+        dt = time.time() - t0
+        durations.append(dt)
+        r = cell["results"]
+        base = f" {args.baseline} {r[args.baseline]['median_ms'] * 1e3:.1f} us" \
+            if args.baseline in r else ""
+        print(f"[{i}/{len(cells)}] {name}: done in {dt:.1f}s; v2 best "
+              f"{r['v2']['median_ms'] * 1e3:.1f} us (ns={r['v2']['best_splits']}), heuristic "
+              f"{r['v2_heuristic']['median_ms'] * 1e3:.1f} us "
+              f"({r['v2_heuristic']['pct_of_sol']:.1f}% SoL){base}; "
+              f"~{(len(cells) - i) * sum(durations) / len(durations) / 60:.1f} min left",
+              flush=True)
+
+    write_summary(out_dir)
+
+
+if __name__ == "__main__":
+    main()
