@@ -12,7 +12,10 @@ Timed region: --ramp-seconds of untimed steps (steady clocks), W untimed
 steps, then K steps bracketed by
 torch.cuda.synchronize(). A v2 step is the C ABI's partial launch followed by
 its merge launch (one launch when num_splits is 1) on the current stream, with
-a caller-owned workspace. HIP events are recorded only between groups of steps
+a caller-owned workspace. With --num-splits 0 (the default) the step is what
+the torch op's automatic choice runs: the token-balanced scan and its merge
+where gqa_decode_prefer_balanced says so (configs 3 and 5), else the split
+heuristic's count. HIP events are recorded only between groups of steps
 (an event between two kernels delays the second):
   value (median us)        median over the groups of the per-step average
   ms_per_step              host wall time of the K steps / K
@@ -55,7 +58,8 @@ def parse_args(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--kernel", default="v2", choices=["v0", "v1", "v2"])
+    ap.add_argument("--kernel", default="v2", choices=["v0", "v1", "v2", "balanced"],
+                    help="v2 with --num-splits 0 makes the op's automatic choice (balanced or split)")
     ap.add_argument("--num-splits", type=int, default=0, help="v2 split count (0 = heuristic)")
     ap.add_argument("--sweep", action="store_true", help="also time v2 over a num_splits sweep")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -85,11 +89,14 @@ def read_traffic(config, kernel, num_splits):
     return None
 
 
-def kernel_name(kernel, group):
-    """The dominant kernel of one step: v0's kernel, else the scan kernel the
-    dispatcher picks for this GQA group size (matrix cores from 5 q-heads)."""
+def kernel_name(kernel, group, balanced=False):
+    """The dominant kernel of one step: v0's kernel, the token-balanced scan,
+    else the scan kernel the dispatcher picks for this GQA group size (matrix
+    cores from 5 q-heads)."""
     if kernel == "v0":
         return "gqa_decode_v0_kernel"
+    if balanced:
+        return "gqa_decode_balanced_kernel"
     return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
 
 
@@ -106,7 +113,7 @@ def main(argv=None):
 
     import capi
     import cases
-    from binding import KERNELS, gqa_decode_v2
+    from binding import KERNELS, gqa_decode_balanced, gqa_decode_v2
 
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -138,10 +145,18 @@ def main(argv=None):
     Hkv, bs, mb = k.shape[2], k.shape[1], bt.shape[1]
 
     ns = args.num_splits
-    if args.kernel == "v2" and ns == 0:
-        ns = capi.pick_num_splits(B, Hq, Hkv, bs, mb, props.multi_processor_count)
+    cus = props.multi_processor_count
+    # v2 with num_splits 0 makes the torch op's automatic choice: the
+    # token-balanced launch where gqa_decode_prefer_balanced says so, else the
+    # split heuristic's count.
+    balanced = args.kernel == "balanced" or (
+        args.kernel == "v2" and ns == 0 and capi.prefer_balanced(B, Hq, Hkv, bs, mb, cus) == 1)
+    if args.kernel == "v2" and ns == 0 and not balanced:
+        ns = capi.pick_num_splits(B, Hq, Hkv, bs, mb, cus)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
+    bal_bytes = capi.balanced_workspace_bytes(B, Hq, Hkv, cus) if balanced else 0
+    bal_ws = torch.empty(max(bal_bytes, 4) // 4, dtype=torch.float32, device=dev)
 
     out = torch.empty_like(q)
     states = B * Hq * max(ns, 1)
@@ -152,6 +167,11 @@ def main(argv=None):
 
     def step_parts():
         """One step as its kernel launches through the C ABI."""
+        if balanced:
+            bal = (*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, cus, bal_ws.data_ptr(),
+                   bal_bytes, sp)
+            return [lambda: capi.balanced_partial_launch(*bal),
+                    lambda: capi.balanced_merge_launch(*bal)]
         if args.kernel == "v2" and ns == 1:
             # One split: the single-pass kernel writes out (and the workspace).
             return [lambda: capi.v2_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, 1,
@@ -219,8 +239,10 @@ def main(argv=None):
         f"wall {wall / K * 1e3:.3f} ms/step")
 
     # The torch operator, timed the reference's way.
-    if args.kernel == "v2":
-        op = lambda: gqa_decode_v2(*case, scale, num_splits=ns)  # noqa: E731
+    if args.kernel == "balanced":
+        op = lambda: gqa_decode_balanced(*case, scale)  # noqa: E731
+    elif args.kernel == "v2":
+        op = lambda: gqa_decode_v2(*case, scale, num_splits=args.num_splits if balanced else ns)  # noqa: E731
     else:
         op = lambda: KERNELS[args.kernel](*case, scale)  # noqa: E731
     op_ms = cases.time_op(op, warmup=3, runs=min(K, 30))
@@ -236,7 +258,8 @@ def main(argv=None):
             sweep[s] = round(ms * 1e3, 2)
             log(f"  sweep num_splits={s}: {ms * 1e3:.2f} us ({sol / (ms * 1e3) * 100:.1f}% SoL)")
 
-    traffic = read_traffic(args.config, args.kernel, ns)
+    split_label = "balanced" if balanced else ns
+    traffic = read_traffic(args.config, "v2" if balanced else args.kernel, split_label)
     achieved = kvb / (kern_avg_us * 1e-6) / 1e9
     result = {
         "metric": METRIC,
@@ -254,13 +277,14 @@ def main(argv=None):
         "data": f"synthetic N(0,1) bf16, seed {args.seed}",
         "config": {"workload": f"{args.config}: {cfg['desc']}", "Hq": Hq, "Hkv": Hkv, "B": B,
                    "S": cfg["S"] if cfg["S"] else "U[1,32768]", "block": bs,
-                   "kernel": args.kernel, "num_splits": ns if args.kernel == "v2" else None},
+                   "kernel": args.kernel,
+                   "num_splits": split_label if args.kernel in ("v2", "balanced") else None},
         "pct_of_sol": round(sol / median_us * 100, 2),
         "achieved_gbps": round(kvb / median_us / 1e3, 1),
         "kv_bytes": kvb,
         "sol_us": round(sol, 3),
         "op_median_us": round(op_ms * 1e3, 3),
-        "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv),
+        "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv, balanced),
                      "achieved": round(achieved, 1),
                      "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
                      "avg_kernel_us": round(kern_avg_us, 3),

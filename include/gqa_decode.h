@@ -121,6 +121,65 @@ GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_split
 GQA_DECODE_API int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size,
                                int max_blocks, int num_cus);
 
+/* Largest GQA group (Hq / Hkv) the token-balanced launcher serves. */
+#define GQA_DECODE_BALANCED_MAX_GROUP 4
+/* Largest batch the token-balanced launcher serves. */
+#define GQA_DECODE_BALANCED_MAX_BATCH 20479
+
+/* Token-balanced split-KV: a persistent grid of num_workgroups workgroups
+ * (<= 0: one per CU of the current device), each taking an equal share of the
+ * batch's 16-token tiles in (request, kv-head) order, whatever the lengths;
+ * segments cut at a share boundary are merged by a second kernel in share
+ * order, so results are bitwise reproducible for a given num_workgroups (and
+ * agree with v1/v2 within rounding, not bitwise). The host never reads
+ * seq_lens. Lengths are clamped to max_blocks * block_size; a request of
+ * length 0 gets NaN. Requires Hq / Hkv <= GQA_DECODE_BALANCED_MAX_GROUP and
+ * B <= GQA_DECODE_BALANCED_MAX_BATCH (else hipErrorInvalidValue), and a
+ * workspace of at least gqa_decode_balanced_workspace_bytes() bytes, 16-byte
+ * aligned, whose contents need no initialisation. No reference counterpart:
+ * the reference's split count is per request (kernels/gqa_decode/
+ * v2_splitkv.cu:30-32); this is its split-KV with splits sized by tokens. */
+GQA_DECODE_API int gqa_decode_balanced_launch(const uint16_t* q, const uint16_t* k_cache,
+                               const uint16_t* v_cache, const int* block_table,
+                               const int* seq_lens, uint16_t* out, int B, int Hq,
+                               int Hkv, int block_size, int max_blocks, float scale,
+                               int num_workgroups, float* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes gqa_decode_balanced_launch needs: two partial states and a
+ * small share record per workgroup. 0 for invalid arguments or an unsupported
+ * group size. */
+GQA_DECODE_API size_t gqa_decode_balanced_workspace_bytes(int B, int Hq, int Hkv,
+                                                          int num_workgroups);
+
+/* The two launches of gqa_decode_balanced_launch, same arguments: _partial
+ * scans every share (writing `out` for whole segments, the workspace for cut
+ * ones), _merge combines the cut segments into `out`. Issued in that order on
+ * one stream they are gqa_decode_balanced_launch; separately they let a
+ * caller time or profile the scan alone. */
+GQA_DECODE_API int gqa_decode_balanced_partial_launch(
+    const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
+    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+    float scale, int num_workgroups, float* workspace, size_t workspace_bytes,
+    hipStream_t stream);
+
+GQA_DECODE_API int gqa_decode_balanced_merge_launch(
+    const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
+    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+    float scale, int num_workgroups, float* workspace, size_t workspace_bytes,
+    hipStream_t stream);
+
+/* 1 if gqa_decode_balanced_launch is expected to beat the split-KV launch with
+ * gqa_decode_pick_num_splits' count for this shape on num_cus CUs (<= 0: the
+ * current device), else 0 (also for shapes the balanced launcher does not
+ * serve). The rule, from measurements on MI355X: groups of at most 4 q-heads,
+ * the split heuristic asking for more than one split, at least 64 MiB of KV
+ * (B * max_blocks * block_size tokens), and at most 4 (request, kv-head)
+ * segments per CU. This is the choice the torch op makes for num_splits=0.
+ * Pure host code. No reference counterpart. */
+GQA_DECODE_API int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size,
+                                              int max_blocks, int num_cus);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,458 @@
+// Token-balanced split-KV decode for gfx950: a persistent grid of one
+// workgroup per CU, each taking an equal share of all the batch's tiles.
+//
+// The split-rule kernels give every request the same number of splits, so in
+// a ragged batch the waves of long requests stream far longer than the rest,
+// and the host cannot size the splits to the lengths without reading seq_lens
+// back. Here the work is the concatenation, in (request, kv-head) order, of
+// every segment's 16-token tiles: T = Hkv * sum_b ceil(S_b / 16) tiles.
+// Workgroup w of nwg takes tiles [w*T/nwg, (w+1)*T/nwg) -- equal shares to
+// within one tile, whatever the lengths -- and walks them segment by segment
+// ("pieces"), scanning each piece with the VALU scan of gqa_scan_valu.hpp
+// (P = 4 waves dealing the piece's tiles round-robin). A piece that is a whole
+// segment is normalised and written to `out` directly; only the first and last
+// piece of a workgroup can be partial, and their states go to two workspace
+// slots. A second kernel merges each segment that was cut at a workgroup
+// boundary, in workgroup order: results are bitwise reproducible for a given
+// nwg.
+//
+// Each workgroup computes the tile prefix sums of the batch itself (from
+// seq_lens, into LDS), so the host needs no lengths and launches a fixed grid.
+// The LDS table is sized so that only one workgroup fits a CU: with nwg = the
+// CU count that gives one wave per SIMD, the residency the split-rule kernels
+// measured fastest. Lengths are clamped to max_blocks * block_size, so no
+// block-table read leaves the request's row; a request of length 0 gets NaN,
+// as 0/0 gives in the other kernels (and the reference).
+#include "gqa_device.hpp"
+#include "gqa_launch.hpp"
+#include "gqa_scan.hpp"
+#include "gqa_scan_valu.hpp"
+#include "gqa_decode.h"
+
+#include <type_traits>
+
+namespace gqa {
+
+// Requests the LDS prefix table holds. 20480 entries (80 KiB) also keep the
+// LDS of one workgroup above half the CU's 160 KiB: one workgroup per CU.
+constexpr int kBalancedTable = 20480;
+constexpr int kBalancedMaxB = GQA_DECODE_BALANCED_MAX_BATCH;
+static_assert(kBalancedMaxB < kBalancedTable, "prefix table holds B + 1 entries");
+constexpr int kStateStride = 132;  // floats per slot state: acc[128], m, l, 2 pad (16-byte rows)
+
+// What the merge kernel needs about the boundary at the end of share w,
+// written by the share's workgroup: the batch's tile count and the segment
+// its last piece belongs to, and whether that boundary cuts the segment and
+// is the first boundary inside it (then the merge starts there).
+struct ShareMeta {
+  int T, seg0, seg1;  // all tiles; the segment's tile range
+  int b, hkv, merge, pad0, pad1;
+};
+
+struct BalancedArgs {
+  float* states;    // [nwg][2][GH][kStateStride]: first-piece and last-piece slots
+  ShareMeta* meta;  // [nwg]
+  int B, nwg, s_cap;
+};
+
+// Workspace layout: the state slots, then the share records (16-byte aligned).
+inline size_t balanced_states_bytes(int nwg, int GH) {
+  return ((size_t)nwg * 2 * GH * kStateStride * sizeof(float) + 15) & ~size_t(15);
+}
+
+// pre[b] = sum over requests b' < b of ceil(min(S_b', s_cap) / 16), for
+// b = 0..B, computed by all NT threads of the workgroup in rounds of NT
+// requests (coalesced loads, wave scans, a carry across rounds).
+template <int NT>
+__device__ __forceinline__ void tile_prefix(const int* __restrict__ seq_lens, int B, int s_cap,
+                                            uint32_t* pre, uint32_t* wave_tot) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int NW = NT / 64;
+  uint32_t carry = 0;
+  if (tid == 0) pre[0] = 0;
+  for (int base = 0; base < B; base += NT) {
+    const int b = base + tid;
+    uint32_t x = 0;
+    if (b < B) {
+      const int s = min(max(seq_lens[b], 0), s_cap);
+      x = (uint32_t)((s + kTile - 1) / kTile);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wave_tot[wv] = x;
+    __syncthreads();
+    uint32_t off = carry, total = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t t = wave_tot[w];
+      off += w < wv ? t : 0;
+      total += t;
+    }
+    if (b < B) pre[b + 1] = off + x;
+    carry += total;
+    __syncthreads();  // wave_tot is rewritten next round; pre is complete after the last
+  }
+}
+
+// The request whose tiles contain global tile t (0 <= t < T): the largest b
+// with Hkv * pre[b] <= t. Requests without tiles are never returned. (The
+// launcher guarantees every tile index, T included, fits in 31 bits.)
+__device__ __forceinline__ int find_request(const uint32_t* pre, int B, int Hkv, int t) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (Hkv * (int)pre[mid] <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Values every lane of the workgroup computed alike from LDS, made uniform
+// for the compiler (scalar registers, scalar block-id loads in the scan).
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ uint32_t uniform(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+
+__device__ __forceinline__ int share_start(int w, int T, int nwg) {
+  return (int)((int64_t)w * T / nwg);
+}
+
+__device__ __forceinline__ int clamped_len(const ScanArgs& a, int b, int s_cap) {
+  return min(max(a.seq_lens[b], 0), s_cap);
+}
+
+template <int GH, int P, int DEPTH, bool kBlockUniform>
+__global__ __launch_bounds__(64 * P) void gqa_decode_balanced_kernel(const ScanArgs a,
+                                                                     const BalancedArgs ba) {
+  __shared__ uint32_t pre[kBalancedTable];
+  __shared__ uint32_t wave_tot[P];
+  __shared__ WaveMergeLds<GH, P> lds;
+  const int lane = threadIdx.x & 63;
+  const int ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 4, c = lane & 15;
+  const int w = blockIdx.x;
+  const int Hkv = a.Hkv, B = ba.B;
+
+  tile_prefix<64 * P>(a.seq_lens, B, ba.s_cap, pre, wave_tot);
+  const int T = Hkv * (int)uniform(pre[B]);
+  const int t0 = share_start(w, T, ba.nwg), t1 = share_start(w + 1, T, ba.nwg);
+
+  // Requests without tokens sit at position Hkv * pre[b] of the tile order;
+  // the first workgroup whose share ends at or after it writes their NaN.
+  for (int b = threadIdx.x; b < B; b += 64 * P) {
+    const int p = Hkv * (int)pre[b];
+    if (pre[b + 1] == pre[b] && t1 >= p && (w == 0 || t0 < p)) {
+      uint32_t* o = reinterpret_cast<uint32_t*>(a.out + (size_t)b * a.Hq * kHeadDim);
+      for (int i = 0; i < a.Hq * kHeadDim / 2; ++i) o[i] = 0x7fc07fc0u;  // bf16 quiet NaN pairs
+    }
+  }
+  if (t0 >= t1) {
+    if (threadIdx.x == 0) ba.meta[w] = ShareMeta{T, 0, 0, 0, 0, 0, 0, 0};
+    return;
+  }
+
+  int b = uniform(find_request(pre, B, Hkv, t0));
+  int req0 = Hkv * (int)uniform(pre[b]);
+  int n = (int)uniform(pre[b + 1] - pre[b]);
+  int hkv = (t0 - req0) / n;
+  const int G = a.G;
+  int t = t0;
+  for (int piece = 0; t < t1; ++piece) {
+    const int seg0 = req0 + hkv * n;
+    const int lt0 = t - seg0;
+    const int lt1 = min(t1, seg0 + n) - seg0;
+    const int S = clamped_len(a, b, ba.s_cap);
+    const int h0 = hkv * G;
+
+    uint4 qf[GH];
+    load_q(a, b, h0, G, c, qf);
+    WaveState<GH> st;
+    init_state(st);
+    scan_segment<GH, P, DEPTH, kBlockUniform>(a, a.block_table + (size_t)b * a.max_blocks, hkv,
+                                              qf, kTile * lt0, min(S, kTile * lt1), ph, r, c, st);
+    float Mw[GH], Lw[GH];
+    merge_rows(st, Mw, Lw);
+    __syncthreads();  // the previous piece's reads of lds are done
+    stage_wave_state(lds, ph, lane, r, c, st, Mw, Lw);
+    __syncthreads();
+
+    const bool whole = lt0 == 0 && lt1 == n;
+    // Only a workgroup's first and last pieces can be partial: slot 0 / 1.
+    float* slot = ba.states + ((size_t)w * 2 + (piece == 0 ? 0 : 1)) * GH * kStateStride;
+    for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 64 * P) {
+      const int h = idx / kHeadDim, d = idx % kHeadDim;
+      float M, L, A;
+      merge_wave_states(lds, h, d, M, L, A);
+      if (whole) {
+        a.out[((size_t)b * a.Hq + h0 + h) * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(finalize(A, L));
+      } else {
+        float* sh = slot + h * kStateStride;
+        sh[d] = A;
+        if (d == 0) {
+          sh[kHeadDim] = M;  // base-2 units
+          sh[kHeadDim + 1] = L;
+        }
+      }
+    }
+
+    // The share's record, at its last piece: the boundary after it cuts the
+    // segment if the piece ends early, and is the segment's first cut (where
+    // the merge starts) if the piece also starts at the segment's start.
+    if (threadIdx.x == 0 && seg0 + lt1 >= t1)
+      ba.meta[w] = ShareMeta{T, seg0, seg0 + n, b, hkv, lt0 == 0 && lt1 < n, 0, 0};
+    t = seg0 + lt1;
+    if (++hkv == Hkv) {
+      hkv = 0;
+      do {
+        ++b;
+      } while (b < B && uniform(pre[b + 1]) == uniform(pre[b]));
+      if (b < B) {
+        req0 = Hkv * (int)uniform(pre[b]);
+        n = (int)uniform(pre[b + 1] - pre[b]);
+      }
+    }
+  }
+}
+
+// Workgroup w merges the segment whose first cut is the boundary after share
+// w (the share's record says so; otherwise it exits at once). The segment's
+// pieces are in shares w .. vend - 1: the first one's in its last-piece slot
+// unless the segment is that share's first piece, every later one's in its
+// first-piece slot. Wave i folds pieces i, i + P, ... in order with an online
+// merge (lane l owns dims 2l, 2l + 1 of every head), loading a batch of pieces
+// before folding it; the P wave results are then combined in wave order:
+// bitwise reproducible.
+template <int GH, int P>
+__global__ __launch_bounds__(64 * P) void gqa_decode_balanced_merge_kernel(const ScanArgs a,
+                                                                           const BalancedArgs ba) {
+  constexpr int kBatch = 4;  // pieces a wave loads together
+  __shared__ WaveMergeLds<GH, P> lds;
+  const int w = blockIdx.x;
+  const ShareMeta meta = ba.meta[w];
+  if (!meta.merge) return;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwg = ba.nwg, G = a.G;
+  const int T = meta.T, seg0 = meta.seg0, seg1 = meta.seg1;
+  // Shares starting before seg1: share_start(v) < seg1 <=> v * T < seg1 * nwg.
+  const int vend = (int)min((int64_t)nwg, ((int64_t)seg1 * nwg + T - 1) / T);
+
+  float M[GH], L[GH];
+  float2 A[GH];
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+    M[h] = kNegInf;
+    L[h] = 0.f;
+    A[h] = make_float2(0.f, 0.f);
+  }
+  for (int v = w + wv; v < vend; v += kBatch * P) {
+    float mv[kBatch][GH], lv[kBatch][GH];
+    float2 av[kBatch][GH];
+    bool live[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int u = v + k * P;
+      const int u0 = share_start(u, T, nwg), u1 = share_start(u + 1, T, nwg);
+      live[k] = u < vend && u1 > u0;  // an empty share holds no piece
+      const float* base = ba.states + ((size_t)(live[k] ? u : w) * 2 + (u0 < seg0 ? 1 : 0)) *
+                                          GH * kStateStride;
+#pragma unroll
+      for (int h = 0; h < GH; ++h) {
+        const float* sh = base + (h < G ? h : 0) * kStateStride;
+        mv[k][h] = sh[kHeadDim];
+        lv[k][h] = sh[kHeadDim + 1];
+        av[k][h] = reinterpret_cast<const float2*>(sh)[lane];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (!live[k]) continue;
+#pragma unroll
+      for (int h = 0; h < GH; ++h) {
+        const float mn = fmaxf(M[h], mv[k][h]);
+        const float ms = mn == kNegInf ? 0.f : mn;
+        const float fa = exp2_fast(M[h] - ms), fv = exp2_fast(mv[k][h] - ms);
+        L[h] = fmaf(L[h], fa, lv[k][h] * fv);
+        A[h].x = fmaf(A[h].x, fa, av[k][h].x * fv);
+        A[h].y = fmaf(A[h].y, fa, av[k][h].y * fv);
+        M[h] = mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+    reinterpret_cast<float2*>(&lds.acc[wv][h][0])[lane] = A[h];
+    if (lane == 0) {
+      lds.m[wv][h] = M[h];
+      lds.l[wv][h] = L[h];
+    }
+  }
+  __syncthreads();
+  const int h0 = meta.hkv * G;
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 64 * P) {
+    const int h = idx / kHeadDim, d = idx % kHeadDim;
+    float Mh, Lh, Ah;
+    merge_wave_states(lds, h, d, Mh, Lh, Ah);
+    a.out[((size_t)meta.b * a.Hq + h0 + h) * kHeadDim + d] =
+        (uint16_t)f32_to_bf16_bits(finalize(Ah, Lh));
+  }
+}
+
+template <int GH>
+hipError_t launch_balanced_partial(const ScanArgs& a, const BalancedArgs& ba, hipStream_t stream) {
+  constexpr int P = kWavesPerHead;
+  if (a.block_size % kTile == 0)
+    hipLaunchKernelGGL((gqa_decode_balanced_kernel<GH, P, kScanDepth, true>), dim3(ba.nwg),
+                       dim3(64 * P), 0, stream, a, ba);
+  else
+    hipLaunchKernelGGL((gqa_decode_balanced_kernel<GH, P, kScanDepth, false>), dim3(ba.nwg),
+                       dim3(64 * P), 0, stream, a, ba);
+  return hipGetLastError();
+}
+
+template <int GH>
+hipError_t launch_balanced_merge(const ScanArgs& a, const BalancedArgs& ba, hipStream_t stream) {
+  constexpr int P = kWavesPerHead;
+  if (ba.nwg < 2) return hipSuccess;  // one share: every piece was whole
+  hipLaunchKernelGGL((gqa_decode_balanced_merge_kernel<GH, P>), dim3(ba.nwg - 1), dim3(64 * P), 0,
+                     stream, a, ba);
+  return hipGetLastError();
+}
+
+int balanced_workgroups(int num_workgroups) {
+  return num_workgroups > 0 ? num_workgroups : device_cu_count();
+}
+
+}  // namespace gqa
+
+extern "C" size_t gqa_decode_balanced_workspace_bytes(int B, int Hq, int Hkv, int num_workgroups) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0) return 0;
+  const int G = Hq / Hkv;
+  if (G > GQA_DECODE_BALANCED_MAX_GROUP) return 0;
+  const int nwg = gqa::balanced_workgroups(num_workgroups);
+  if (nwg <= 0) return 0;
+  return gqa::balanced_states_bytes(nwg, gqa::heads_per_wave(G)) +
+         (size_t)nwg * sizeof(gqa::ShareMeta);
+}
+
+namespace {
+
+enum class BalancedPart { kBoth, kPartial, kMerge };
+
+// Checks, argument packing and launch of one or both balanced kernels.
+int balanced_launch(BalancedPart part, const uint16_t* q, const uint16_t* k_cache,
+                    const uint16_t* v_cache, const int* block_table, const int* seq_lens,
+                    uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+                    float scale, int num_workgroups, float* workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
+  hipError_t err = gqa::check_common(q, k_cache, v_cache, block_table, seq_lens, out, B, Hq, Hkv,
+                                     block_size, max_blocks);
+  if (err != hipSuccess) return err;
+  if (B == 0) return hipSuccess;
+  const int G = Hq / Hkv;
+  if (G > GQA_DECODE_BALANCED_MAX_GROUP || B > gqa::kBalancedMaxB) return hipErrorInvalidValue;
+  const int64_t s_cap = (int64_t)max_blocks * block_size;
+  // Every tile index of the batch, Hkv * sum_b ceil(S_b / 16), fits in 31 bits.
+  if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  const int nwg = gqa::balanced_workgroups(num_workgroups);
+  if (nwg <= 0) return hipErrorInvalidValue;
+  if (!workspace || workspace_bytes < gqa_decode_balanced_workspace_bytes(B, Hq, Hkv, nwg))
+    return hipErrorInvalidValue;
+
+  gqa::ScanArgs a{};
+  a.q = q;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.block_table = block_table;
+  a.seq_lens = seq_lens;
+  a.out = out;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = G;
+  a.nchunk = 1;
+  a.block_size = block_size;
+  a.max_blocks = max_blocks;
+  a.num_splits = 1;
+  a.bs_div = gqa::make_fastdiv((uint32_t)block_size);
+  a.scale_log2e = (float)((double)scale * 1.4426950408889634);
+  const size_t states = gqa::balanced_states_bytes(nwg, gqa::heads_per_wave(G));
+  const gqa::BalancedArgs ba{workspace,
+                             reinterpret_cast<gqa::ShareMeta*>(
+                                 reinterpret_cast<char*>(workspace) + states),
+                             B, nwg, (int)s_cap};
+  auto run = [&](auto gh) -> int {
+    constexpr int GH = decltype(gh)::value;
+    if (part != BalancedPart::kMerge) {
+      const hipError_t e = gqa::launch_balanced_partial<GH>(a, ba, stream);
+      if (e != hipSuccess || part == BalancedPart::kPartial) return e;
+    }
+    return gqa::launch_balanced_merge<GH>(a, ba, stream);
+  };
+  switch (gqa::heads_per_wave(G)) {
+    case 1: return run(std::integral_constant<int, 1>{});
+    case 2: return run(std::integral_constant<int, 2>{});
+    default: return run(std::integral_constant<int, 4>{});
+  }
+}
+
+}  // namespace
+
+extern "C" int gqa_decode_balanced_launch(const uint16_t* q, const uint16_t* k_cache,
+                                          const uint16_t* v_cache, const int* block_table,
+                                          const int* seq_lens, uint16_t* out, int B, int Hq,
+                                          int Hkv, int block_size, int max_blocks, float scale,
+                                          int num_workgroups, float* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+  return balanced_launch(BalancedPart::kBoth, q, k_cache, v_cache, block_table, seq_lens, out, B,
+                         Hq, Hkv, block_size, max_blocks, scale, num_workgroups, workspace,
+                         workspace_bytes, stream);
+}
+
+extern "C" int gqa_decode_balanced_partial_launch(
+    const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
+    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+    float scale, int num_workgroups, float* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+  return balanced_launch(BalancedPart::kPartial, q, k_cache, v_cache, block_table, seq_lens, out,
+                         B, Hq, Hkv, block_size, max_blocks, scale, num_workgroups, workspace,
+                         workspace_bytes, stream);
+}
+
+extern "C" int gqa_decode_balanced_merge_launch(
+    const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
+    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+    float scale, int num_workgroups, float* workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+  return balanced_launch(BalancedPart::kMerge, q, k_cache, v_cache, block_table, seq_lens, out, B,
+                         Hq, Hkv, block_size, max_blocks, scale, num_workgroups, workspace,
+                         workspace_bytes, stream);
+}
+
+extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size, int max_blocks,
+                                          int num_cus) {
+  // Measured on MI355X: the token-balanced launch wins where per-request splits
+  // are uneven (ragged lengths, or a split count the length bound forces on a
+  // grid that was already full) and costs a few microseconds of fixed
+  // overhead (prefix sums, a second launch) where they are even. It is
+  // preferred when the split heuristic would split at all (one split means
+  // the grid already holds exactly one round of whole segments), the batch
+  // holds at least kMinBytes of KV (so the overhead stays small), and there
+  // are at most kMaxSegmentsPerCu segments per workgroup (each piece restarts
+  // the load pipeline).
+  constexpr int64_t kMinBytes = int64_t(64) << 20;
+  constexpr int kMaxSegmentsPerCu = 4;
+  if (num_cus <= 0 && (num_cus = gqa::device_cu_count()) <= 0) return 0;
+  if (B < 1 || Hkv < 1 || Hq % Hkv != 0 || Hq / Hkv > GQA_DECODE_BALANCED_MAX_GROUP ||
+      B > gqa::kBalancedMaxB || block_size < 1 || max_blocks < 1)
+    return 0;
+  const int64_t s_cap = (int64_t)max_blocks * block_size;
+  if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31)) return 0;
+  if (gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus) <= 1) return 0;
+  if ((int64_t)B * s_cap * Hkv * gqa::kHeadDim * 4 < kMinBytes) return 0;
+  return (int64_t)B * Hkv <= (int64_t)kMaxSegmentsPerCu * num_cus ? 1 : 0;
+}

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace gqa {
 
 // The checks python/gqa_decode_ext.cpp:16-62 makes on tensor shapes, restated
@@ -22,6 +24,21 @@ inline hipError_t check_common(const void* q, const void* k_cache, const void* v
   if (B > 0 && (!q || !k_cache || !v_cache || !block_table || !seq_lens || !out))
     return hipErrorInvalidValue;
   return hipSuccess;
+}
+
+// CU count of the current device, queried once per device (a racing first
+// query stores the same value); 0 if it cannot be queried.
+inline int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  int cus = dev >= 0 && dev < 64 ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 0;
+  if (dev >= 0 && dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
 }
 
 }  // namespace gqa

@@ -1,0 +1,284 @@
+// The VALU scan of one (request, kv-head) segment by a workgroup of P waves:
+// tile loads, QK^T / online softmax / PV per tile, and the fixed-order merges
+// of row and wave states. Shared by the split-rule kernels
+// (gqa_decode_split.hip) and the token-balanced persistent kernel
+// (gqa_decode_balanced.hip); everything here is force-inlined into them.
+//
+// A wave's 64 lanes form 4 DPP rows of 16 lanes; a row reads one 256-byte K
+// (or V) head row with 16-byte loads, so one load instruction covers 4 tokens
+// and a 16-token tile is 4 K loads + 4 V loads per lane. Per tile: QK^T with
+// v_dot2c_f32_bf16 on the packed bf16 q and K words, a 4-step DPP row
+// reduction, then one online-softmax update per (row, head) for the whole tile
+// (max over its 4 tokens, one rescale of l and acc) in base-2 units, and PV as
+// fp32 FMAs. The next tile's loads are issued before the current tile is
+// consumed.
+#pragma once
+
+#include "gqa_device.hpp"
+#include "gqa_scan.hpp"
+
+namespace gqa {
+
+constexpr int kTile = 16;        // tokens per wave per tile
+constexpr int kChunkAlign = 32;  // split lengths are multiples of this (both split-rule kernels)
+constexpr int kLoads = 4;        // 16-byte K loads (and V loads) per lane per tile
+
+// Launch shapes. A workgroup holds P waves that share one kv-head, take its
+// 16-token tiles round-robin and merge their states through LDS. Measured on
+// MI355X: the stream runs fastest with about one wave per SIMD resident (4 per
+// CU), each keeping one tile in flight while it consumes the previous one;
+// more resident waves or deeper prefetch only add queueing. P = 4 waves per
+// kv-head keeps a workgroup's reads adjacent and the merge in LDS.
+constexpr int kWavesPerHead = 4;  // P: waves sharing a kv-head (all scan kernels)
+constexpr int kScanDepth = 2;     // register tiles in flight per wave
+
+struct TileRegs {
+  uint4 k[kLoads];
+  uint4 v[kLoads];
+};
+
+// Online-softmax state of GH q-heads in one lane: m and l per head (identical
+// across the 16 lanes of a DPP row), acc over the lane's 8 dims.
+template <int GH>
+struct WaveState {
+  float m[GH], l[GH], acc[GH][8];
+};
+
+template <int GH>
+__device__ __forceinline__ void init_state(WaveState<GH>& st) {
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    st.m[j] = kNegInf;
+    st.l[j] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[j][d] = 0.f;
+  }
+}
+
+// q rows of heads h0 .. h0 + nh - 1 of request b: lane dims [8c, 8c + 8);
+// heads past nh are zero (their results are never written).
+template <int GH>
+__device__ __forceinline__ void load_q(const ScanArgs& a, int b, int h0, int nh, int c,
+                                       uint4 (&qf)[GH]) {
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    qf[j] = make_uint4(0, 0, 0, 0);
+    if (j < nh)
+      qf[j] = *reinterpret_cast<const uint4*>(a.q + ((size_t)b * a.Hq + h0 + j) * kHeadDim + 8 * c);
+  }
+}
+
+// Scan tokens [seg_start, seg_end) of kv-head hkv of the request whose block
+// table row is bt: wave ph of the P takes tiles ph, ph + P, ... of the range and
+// folds them into st. DEPTH register tiles are in flight; the steady-state
+// loop issues tile k + DEPTH - 1 before consuming tile k and has no branch, so
+// the wait before each consume covers only the tile being consumed.
+template <int GH, int P, int DEPTH, bool kBlockUniform>
+__device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, int hkv,
+                                             const uint4 (&qf)[GH], int seg_start, int seg_end,
+                                             int ph, int r, int c, WaveState<GH>& st) {
+  const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
+  const int my_tiles = ntiles > ph ? (ntiles - ph + P - 1) / P : 0;
+  const uint32_t row_elems = (uint32_t)a.Hkv * kHeadDim;  // elements between slots
+  const uint16_t* kbase = a.k_cache + (size_t)hkv * kHeadDim + 8 * c;
+  const uint16_t* vbase = a.v_cache + (size_t)hkv * kHeadDim + 8 * c;
+  const int bs = a.block_size;
+  // The block table is read-only for the whole launch: reading it through the
+  // constant address space lets the uniform block-id loads stay scalar even
+  // in kernels that store to global memory between segments.
+  const __attribute__((address_space(4))) int* btc =
+      (const __attribute__((address_space(4))) int*)bt;
+
+  auto tile_start = [&](int k) { return seg_start + kTile * (ph + P * k); };
+
+  // Issue the K and V loads of this wave's tile k. Tokens at or past seg_end
+  // read the tile's first token instead (always valid), so no load touches an
+  // unallocated block or a tail slot; their scores are masked in consume().
+  auto issue = [&](int k, TileRegs& t) {
+    const int ts = tile_start(k);
+    if constexpr (kBlockUniform) {
+      // The 16 tokens of the tile share one block: scalar block-id load, a
+      // uniform 64-bit block base and 32-bit per-lane offsets inside it.
+      const uint32_t lb = fastdiv((uint32_t)ts, a.bs_div);
+      const int slot0 = ts - (int)lb * bs;
+      const size_t blk = (size_t)btc[lb] * ((size_t)bs * row_elems) + (size_t)hkv * kHeadDim;
+      const uint16_t* kblk = a.k_cache + blk;
+      const uint16_t* vblk = a.v_cache + blk;
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) {
+        const int tok = ts + 4 * j + r;
+        const uint32_t slot = tok < seg_end ? slot0 + 4 * j + r : slot0;
+        const uint32_t off = slot * row_elems + 8 * c;
+        t.k[j] = *reinterpret_cast<const uint4*>(kblk + off);
+        t.v[j] = *reinterpret_cast<const uint4*>(vblk + off);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) {
+        int tok = ts + 4 * j + r;
+        tok = tok < seg_end ? tok : ts;
+        const uint32_t lb = fastdiv((uint32_t)tok, a.bs_div);
+        const int slot = tok - (int)lb * bs;
+        const size_t off = ((size_t)bt[lb] * bs + slot) * row_elems;
+        t.k[j] = *reinterpret_cast<const uint4*>(kbase + off);
+        t.v[j] = *reinterpret_cast<const uint4*>(vbase + off);
+      }
+    }
+  };
+
+  auto consume = [&](int k, const TileRegs& t) {
+    const int ts = tile_start(k);
+    float s[kLoads][GH];  // scores (base-2 units), then probabilities
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const bool valid = ts + 4 * j + r < seg_end;
+#pragma unroll
+      for (int h = 0; h < GH; ++h) {
+        float d = dot2_bf16(qf[h].x, t.k[j].x, 0.f);
+        d = dot2_bf16(qf[h].y, t.k[j].y, d);
+        d = dot2_bf16(qf[h].z, t.k[j].z, d);
+        d = dot2_bf16(qf[h].w, t.k[j].w, d);
+        d = row16_sum(d);
+        s[j][h] = valid ? d * a.scale_log2e : kNegInf;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
+      const float mn = fmaxf(st.m[h], mt);
+      const float ms = mn == kNegInf ? 0.f : mn;  // a row with no valid token yet
+      const float al = exp2_fast(st.m[h] - ms);
+      st.m[h] = mn;
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) s[j][h] = exp2_fast(s[j][h] - ms);
+      st.l[h] = fmaf(st.l[h], al, (s[0][h] + s[1][h]) + (s[2][h] + s[3][h]));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) st.acc[h][d] *= al;
+    }
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const float vf[8] = {bf16_lo(t.v[j].x), bf16_hi(t.v[j].x), bf16_lo(t.v[j].y),
+                           bf16_hi(t.v[j].y), bf16_lo(t.v[j].z), bf16_hi(t.v[j].z),
+                           bf16_lo(t.v[j].w), bf16_hi(t.v[j].w)};
+#pragma unroll
+      for (int h = 0; h < GH; ++h)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) st.acc[h][d] = fmaf(s[j][h], vf[d], st.acc[h][d]);
+    }
+  };
+
+  if (my_tiles > 0) {
+    TileRegs t[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i)
+      if (i < my_tiles) issue(i, t[i]);
+    int k = 0;
+    for (; k + 2 * DEPTH - 2 < my_tiles; k += DEPTH) {
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
+        consume(k + i, t[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) {
+      if (k + i < my_tiles) {
+        if (k + i + DEPTH - 1 < my_tiles) issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
+        consume(k + i, t[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) {
+      // At most 2*DEPTH - 2 tiles remain after the loop; the block above
+      // consumed DEPTH of them.
+      if (k + DEPTH + i < my_tiles) {
+        if (k + DEPTH + i + DEPTH - 1 < my_tiles)
+          issue(k + DEPTH + i + DEPTH - 1, t[(i + 2 * DEPTH - 1) % DEPTH]);
+        consume(k + DEPTH + i, t[(DEPTH + i) % DEPTH]);
+      }
+    }
+  }
+}
+
+// Merge the 4 row states of the wave in place (every row ends with the same
+// totals): Mw / Lw get the wave's max and sum, st.acc the rescaled sums.
+template <int GH>
+__device__ __forceinline__ void merge_rows(WaveState<GH>& st, float (&Mw)[GH], float (&Lw)[GH]) {
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+    const float mr = st.m[h];
+    float M = fmaxf(mr, __shfl_xor(mr, 16, 64));
+    M = fmaxf(M, __shfl_xor(M, 32, 64));
+    const float f = mr == M ? 1.f : exp2_fast(mr - (M == kNegInf ? 0.f : M));
+    float lr = st.l[h] * f;
+    lr += __shfl_xor(lr, 16, 64);
+    lr += __shfl_xor(lr, 32, 64);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      float x = st.acc[h][d] * f;
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      st.acc[h][d] = x;
+    }
+    Mw[h] = M;
+    Lw[h] = lr;
+  }
+}
+
+// LDS staging of the P wave states of a workgroup (acc first: its rows take
+// 16-byte stores).
+template <int GH, int P>
+struct WaveMergeLds {
+  float acc[P][GH][kHeadDim];
+  float m[P][GH];
+  float l[P][GH];
+};
+
+// Wave ph stores its merged state (row 0 holds it after merge_rows).
+template <int GH, int P>
+__device__ __forceinline__ void stage_wave_state(WaveMergeLds<GH, P>& lds, int ph, int lane,
+                                                 int r, int c, const WaveState<GH>& st,
+                                                 const float (&Mw)[GH], const float (&Lw)[GH]) {
+#pragma unroll
+  for (int h = 0; h < GH; ++h) {
+    if (r == 0) {
+      float4* dst = reinterpret_cast<float4*>(&lds.acc[ph][h][8 * c]);
+      dst[0] = make_float4(st.acc[h][0], st.acc[h][1], st.acc[h][2], st.acc[h][3]);
+      dst[1] = make_float4(st.acc[h][4], st.acc[h][5], st.acc[h][6], st.acc[h][7]);
+    }
+    if (lane == 0) {
+      lds.m[ph][h] = Mw[h];
+      lds.l[ph][h] = Lw[h];
+    }
+  }
+}
+
+// Combine the P staged wave states of head h at dim d in wave order:
+// M = max, L = sum of rescaled l, A = sum of rescaled acc. The factor of a wave
+// holding the max is exactly 1. M is in base-2 units.
+template <int GH, int P>
+__device__ __forceinline__ void merge_wave_states(const WaveMergeLds<GH, P>& lds, int h, int d,
+                                                  float& M, float& L, float& A) {
+  M = lds.m[0][h];
+#pragma unroll
+  for (int w = 1; w < P; ++w) M = fmaxf(M, lds.m[w][h]);
+  const float Ms = M == kNegInf ? 0.f : M;
+#pragma unroll
+  for (int w = 0; w < P; ++w) {
+    const float mw = lds.m[w][h];
+    const float f = mw == M ? 1.f : exp2_fast(mw - Ms);
+    if (w == 0) {
+      L = lds.l[0][h] * f;
+      A = lds.acc[0][h][d] * f;
+    } else {
+      L = fmaf(lds.l[w][h], f, L);
+      A = fmaf(lds.acc[w][h][d], f, A);
+    }
+  }
+}
+
+// q-heads served per wave of the VALU scan: the whole group (at most 4 here),
+// rounded up to a power of two; extra heads carry q = 0 and are not written.
+inline int heads_per_wave(int G) { return G <= 1 ? 1 : G <= 2 ? 2 : 4; }
+
+}  // namespace gqa

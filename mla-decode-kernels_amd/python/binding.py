@@ -37,6 +37,10 @@ gqa_decode_v0 = _ext.gqa_decode_v0
 gqa_decode_v1 = _ext.gqa_decode_v1
 gqa_decode_v2 = _ext.gqa_decode_v2
 num_splits_heuristic = _ext.num_splits_heuristic
+# Beyond the reference: the token-balanced split-KV launch, and the rule the
+# v2 op's num_splits=0 uses to choose it.
+gqa_decode_balanced = _ext.gqa_decode_balanced
+prefer_balanced = _ext.prefer_balanced
 
 # "v2" runs with its default num_splits=8; pass num_splits explicitly via
 # gqa_decode_v2 to override (0 = heuristic).

@@ -54,6 +54,16 @@ def lib():
         L.gqa_decode_v2_workspace_bytes.restype = ctypes.c_size_t
         L.gqa_decode_pick_num_splits.argtypes = [_i, _i, _i, _i, _i, _i]
         L.gqa_decode_pick_num_splits.restype = _i
+        L.gqa_decode_balanced_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
+        L.gqa_decode_balanced_launch.restype = _i
+        L.gqa_decode_balanced_workspace_bytes.argtypes = [_i, _i, _i, _i]
+        L.gqa_decode_balanced_workspace_bytes.restype = ctypes.c_size_t
+        for name in ("gqa_decode_balanced_partial_launch", "gqa_decode_balanced_merge_launch"):
+            fn = getattr(L, name)
+            fn.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
+            fn.restype = _i
+        L.gqa_decode_prefer_balanced.argtypes = [_i, _i, _i, _i, _i, _i]
+        L.gqa_decode_prefer_balanced.restype = _i
         _lib = L
     return _lib
 
@@ -84,3 +94,23 @@ def workspace_bytes(B, Hq, num_splits):
 
 def pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus):
     return lib().gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus)
+
+
+def balanced_launch(*args):
+    return lib().gqa_decode_balanced_launch(*args)
+
+
+def balanced_workspace_bytes(B, Hq, Hkv, num_workgroups):
+    return lib().gqa_decode_balanced_workspace_bytes(B, Hq, Hkv, num_workgroups)
+
+
+def balanced_partial_launch(*args):
+    return lib().gqa_decode_balanced_partial_launch(*args)
+
+
+def balanced_merge_launch(*args):
+    return lib().gqa_decode_balanced_merge_launch(*args)
+
+
+def prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus):
+    return lib().gqa_decode_prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus)

@@ -8,7 +8,10 @@
 // split-count heuristic (widening the accepted domain [1, 512] of :102-103),
 // a check of the launcher's return code, one workspace allocation carved
 // into the three arrays instead of three, and none at all for one split (the
-// single-pass kernel runs instead, with bitwise the same output).
+// single-pass kernel runs instead, with bitwise the same output). With
+// num_splits == 0 the op runs the token-balanced launch where
+// gqa_decode_prefer_balanced says so, else the split heuristic's count; the
+// balanced launch is also its own op (gqa_decode_balanced).
 //
 // This file is host-only C++ (compiled by g++); all device code lives in the
 // hipcc-built libgqa_decode_hip.so it links against.
@@ -109,7 +112,7 @@ torch::Tensor gqa_decode_v1(torch::Tensor q, torch::Tensor k_cache, torch::Tenso
                         block_table, seq_lens, scale);
 }
 
-int64_t pick_num_splits(const GqaDims& d, const torch::Tensor& q) {
+int device_cus(const torch::Tensor& q) {
   // CU count per device, queried once (a racing first query stores the same value).
   static std::atomic<int> cu_count[64];
   const int dev = q.device().index();
@@ -120,8 +123,30 @@ int64_t pick_num_splits(const GqaDims& d, const torch::Tensor& q) {
                 "could not query the CU count of device ", dev);
     if (dev >= 0 && dev < 64) cu_count[dev].store(cus, std::memory_order_relaxed);
   }
-  return gqa_decode_pick_num_splits((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
-                                    (int)d.max_blocks, cus);
+  return cus;
+}
+
+// The token-balanced launch on the current device (caller holds the guard):
+// one workspace allocation, out from the caching allocator.
+torch::Tensor run_balanced(const GqaDims& d, const torch::Tensor& q, const torch::Tensor& k_cache,
+                           const torch::Tensor& v_cache, const torch::Tensor& block_table,
+                           const torch::Tensor& seq_lens, double scale, int64_t num_workgroups) {
+  const int nwg = num_workgroups > 0 ? (int)num_workgroups : device_cus(q);
+  const size_t bytes = gqa_decode_balanced_workspace_bytes((int)d.B, (int)d.Hq, (int)d.Hkv, nwg);
+  TORCH_CHECK(bytes > 0, "the balanced launch serves GQA groups of at most ",
+              GQA_DECODE_BALANCED_MAX_GROUP, " q-heads");
+  auto out = torch::empty_like(q);
+  auto ws = torch::empty({(int64_t)((bytes + 3) / 4)},
+                         torch::TensorOptions().dtype(torch::kFloat32).device(q.device()));
+  hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+  check_launch(gqa_decode_balanced_launch(bf16_ptr(q), bf16_ptr(k_cache), bf16_ptr(v_cache),
+                                          block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+                                          reinterpret_cast<uint16_t*>(out.data_ptr()), (int)d.B,
+                                          (int)d.Hq, (int)d.Hkv, (int)d.block_size,
+                                          (int)d.max_blocks, (float)scale, nwg,
+                                          ws.data_ptr<float>(), bytes, stream),
+               "gqa_decode_balanced_launch");
+  return out;
 }
 
 torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
@@ -131,7 +156,17 @@ torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tenso
   TORCH_CHECK(num_splits >= 0 && num_splits <= GQA_DECODE_MAX_SPLITS,
               "num_splits must be in [1, 512] (or 0 for the heuristic)");
   const c10::DeviceGuard guard(q.device());
-  if (num_splits == 0) num_splits = d.B > 0 ? pick_num_splits(d, q) : 1;
+  if (num_splits == 0 && d.B > 0) {
+    // Automatic choice: the token-balanced launch where the split launch's
+    // per-request splits would be uneven, else the split heuristic's count.
+    const int cus = device_cus(q);
+    if (gqa_decode_prefer_balanced((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
+                                   (int)d.max_blocks, cus))
+      return run_balanced(d, q, k_cache, v_cache, block_table, seq_lens, scale, 0);
+    num_splits = gqa_decode_pick_num_splits((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
+                                            (int)d.max_blocks, cus);
+  }
+  if (num_splits == 0) num_splits = 1;  // empty batch
   TORCH_CHECK(num_splits >= 1, "num_splits heuristic failed");
 
   if (num_splits == 1) {
@@ -158,10 +193,26 @@ torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tenso
   return out;
 }
 
+torch::Tensor gqa_decode_balanced(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                                  torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                                  int64_t num_workgroups) {
+  const GqaDims d = check_inputs(q, k_cache, v_cache, block_table, seq_lens);
+  TORCH_CHECK(num_workgroups >= 0, "num_workgroups must be >= 0 (0: one per CU)");
+  const c10::DeviceGuard guard(q.device());
+  if (d.B == 0) return torch::empty_like(q);
+  return run_balanced(d, q, k_cache, v_cache, block_table, seq_lens, scale, num_workgroups);
+}
+
 int64_t gqa_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t block_size,
                               int64_t max_blocks, int64_t num_cus) {
   return gqa_decode_pick_num_splits((int)B, (int)Hq, (int)Hkv, (int)block_size, (int)max_blocks,
                                     (int)num_cus);
+}
+
+bool gqa_decode_balanced_preferred(int64_t B, int64_t Hq, int64_t Hkv, int64_t block_size,
+                                   int64_t max_blocks, int64_t num_cus) {
+  return gqa_decode_prefer_balanced((int)B, (int)Hq, (int)Hkv, (int)block_size, (int)max_blocks,
+                                    (int)num_cus) != 0;
 }
 
 }  // namespace
@@ -172,6 +223,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gqa_decode_v2", &gqa_decode_v2, "GQA decode v2 split-KV kernel (paged KV, bf16)",
         py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"),
         py::arg("seq_lens"), py::arg("scale"), py::arg("num_splits") = 8);
+  m.def("gqa_decode_balanced", &gqa_decode_balanced,
+        "token-balanced split-KV decode (paged KV, bf16; GQA groups of at most 4)",
+        py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"),
+        py::arg("seq_lens"), py::arg("scale"), py::arg("num_workgroups") = 0);
+  m.def("prefer_balanced", &gqa_decode_balanced_preferred,
+        "gqa_decode_prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus)", py::arg("B"),
+        py::arg("Hq"), py::arg("Hkv"), py::arg("block_size"), py::arg("max_blocks"),
+        py::arg("num_cus") = 0);
   m.def("num_splits_heuristic", &gqa_decode_num_splits,
         "gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus)",
         py::arg("B"), py::arg("Hq"), py::arg("Hkv"), py::arg("block_size"),

@@ -24,6 +24,9 @@ def test_library_exports_every_declared_function():
         "gqa_decode_v0_launch", "gqa_decode_v1_launch", "gqa_decode_v2_launch",
         "gqa_decode_v2_partial_launch", "gqa_decode_v2_merge_launch",
         "gqa_decode_v2_workspace_bytes", "gqa_decode_pick_num_splits",
+        "gqa_decode_balanced_launch", "gqa_decode_balanced_workspace_bytes",
+        "gqa_decode_balanced_partial_launch", "gqa_decode_balanced_merge_launch",
+        "gqa_decode_prefer_balanced",
     ])
     lib = capi.lib()
     for name in declared:
@@ -152,11 +155,81 @@ def test_v2_rejects_missing_workspace(which):
     assert capi.v2_merge_launch(*ws, FAKE, 2, 32, 8, None) == INVALID
 
 
+@pytest.mark.parametrize("Hq,Hkv,nwg,gh", [(32, 8, 256, 4), (8, 8, 256, 1), (16, 8, 7, 2),
+                                          (24, 8, 256, 4), (4, 1, 1, 4)])
+def test_balanced_workspace_bytes(Hq, Hkv, nwg, gh):
+    # Two partial states (first and last piece) per workgroup, 132 floats per
+    # head, then a 32-byte share record per workgroup at a 16-byte boundary.
+    states = (nwg * 2 * gh * 132 * 4 + 15) // 16 * 16
+    assert capi.balanced_workspace_bytes(32, Hq, Hkv, nwg) == states + nwg * 32
+
+
+@pytest.mark.parametrize("args", [(0, 32, 8, 256), (32, 64, 8, 256), (32, 30, 8, 256),
+                                  (32, 32, 0, 256)])
+def test_balanced_workspace_bytes_invalid(args):
+    assert capi.balanced_workspace_bytes(*args) == 0
+
+
+def balanced_args(ws_bytes=1 << 20, nwg=256, **over):
+    return launch_args(**over) + [nwg, FAKE, ws_bytes, None]
+
+
+@pytest.mark.parametrize("over", BAD)
+def test_balanced_rejects_bad_arguments(over):
+    assert capi.balanced_launch(*balanced_args(**over)) == INVALID
+
+
+def test_balanced_rejects_unsupported_shapes():
+    # Groups above 4 q-heads, batches beyond the LDS prefix table, workspace
+    # missing or too small for the workgroup count.
+    assert capi.balanced_launch(*balanced_args(Hq=64)) == INVALID
+    assert capi.balanced_launch(*balanced_args(B=20480)) == INVALID
+    args = balanced_args()
+    args[-3] = None
+    assert capi.balanced_launch(*args) == INVALID
+    need = capi.balanced_workspace_bytes(2, 32, 8, 256)
+    assert capi.balanced_launch(*balanced_args(ws_bytes=need - 1)) == INVALID
+
+
+@pytest.mark.parametrize("fn", ["balanced_partial_launch", "balanced_merge_launch"])
+@pytest.mark.parametrize("over", BAD + [dict(Hq=64), dict(B=20480)])
+def test_balanced_parts_reject_bad_arguments(fn, over):
+    assert getattr(capi, fn)(*balanced_args(**over)) == INVALID
+
+
+def test_prefer_balanced_headline_shapes():
+    # BASELINE configs 1..5 on 256 CUs: balanced for the long/ragged 4-head
+    # configs (3, 5); the split path where one split already fills the chip
+    # (2), for 8-head groups (4) and for tiny batches (1).
+    shapes = [(1, 32, 16, 32), (32, 32, 16, 512), (8, 32, 64, 512), (32, 64, 64, 512),
+              (128, 32, 16, 2048)]
+    assert [capi.prefer_balanced(B, Hq, 8, bs, mb, 256) for B, Hq, bs, mb in shapes] == \
+        [0, 0, 1, 0, 1]
+
+
+@pytest.mark.parametrize("B,Hq,bs,mb", [(1, 32, 16, 2048), (8, 32, 16, 512), (32, 32, 64, 512),
+                                        (128, 32, 16, 2048), (256, 32, 16, 2048), (1, 32, 16, 64),
+                                        (4, 16, 16, 4096), (2, 64, 16, 4096)])
+def test_prefer_balanced_rule(B, Hq, bs, mb):
+    # The documented rule, clause by clause.
+    Hkv, cus = 8, 256
+    want = (Hq // Hkv <= 4 and capi.pick_num_splits(B, Hq, Hkv, bs, mb, cus) > 1
+            and B * mb * bs * Hkv * 512 >= 64 << 20 and B * Hkv <= 4 * cus)
+    assert capi.prefer_balanced(B, Hq, Hkv, bs, mb, cus) == int(want)
+
+
+def test_prefer_balanced_invalid():
+    assert capi.prefer_balanced(0, 32, 8, 16, 512, 256) == 0
+    assert capi.prefer_balanced(8, 30, 8, 16, 512, 256) == 0
+    assert capi.prefer_balanced(20480, 32, 8, 16, 16, 256) == 0
+
+
 def test_empty_batch_is_a_no_op():
     args = launch_args(B=0, q=None, k=None, v=None, bt=None, sl=None, out=None)
     assert capi.v0_launch(*args, None) == capi.HIP_SUCCESS
     assert capi.v1_launch(*args, None) == capi.HIP_SUCCESS
     assert capi.v2_launch(*args, 8, None, None, None, None) == capi.HIP_SUCCESS
+    assert capi.balanced_launch(*args, 256, None, 0, None) == capi.HIP_SUCCESS
 
 
 # ----------------------------------------------------------- torch operator

@@ -1,0 +1,152 @@
+"""GPU parity of the token-balanced split-KV launcher (gqa_decode_balanced_launch).
+
+Same inputs, poisoning and tolerance as the reference's kernel tests
+(tests/test_gqa_decode.py:27-139 of the reference: 0.5 * N(0,1), shuffled 2x
+pool, NaN in every slot that must not be read, atol = rtol = 2e-2), against
+the oracle, through the C ABI with a caller-owned workspace. Covers the
+reference's case grid for groups up to 4, block sizes that are not multiples
+of 16, workgroup counts from 1 (no merge) to more workgroups than tiles
+(empty shares), ragged batches with zero-length requests (NaN rows, the other
+rows exact), batches longer than one prefix-scan round, bitwise
+repeatability, and the G <= 4 BASELINE configs at full size (1e-2).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import capi
+from binding import gqa_decode_balanced, gqa_decode_v2, prefer_balanced
+from cases import config_seq_lens, make_case, make_config_case
+from gpu_util import assert_close, numpy_oracle, oracle
+from test_gqa_decode import CASES, ref_case
+
+pytestmark = pytest.mark.gpu
+
+ATOL = RTOL = 2e-2
+SCALE = 1.0 / math.sqrt(128)
+
+
+def balanced(case, scale=SCALE, nwg=0, out=None, parts=False):
+    q, k, v, bt, sl = case
+    B, Hq = q.shape[:2]
+    Hkv, bs = k.shape[2], k.shape[1]
+    nbytes = capi.balanced_workspace_bytes(B, Hq, Hkv, nwg)
+    assert nbytes > 0
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+    out = torch.empty_like(q) if out is None else out
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(), out.data_ptr(),
+            B, Hq, Hkv, bs, bt.shape[1], scale, nwg, ws.data_ptr(), nbytes,
+            torch.cuda.current_stream().cuda_stream)
+    if parts:
+        assert capi.balanced_partial_launch(*args) == 0
+        assert capi.balanced_merge_launch(*args) == 0
+    else:
+        assert capi.balanced_launch(*args) == 0
+    torch.cuda.synchronize()
+    return out
+
+
+GRID = {k: v for k, v in CASES.items() if v["Hq"] // v["Hkv"] <= 4}
+
+
+@pytest.mark.parametrize("name", list(GRID))
+def test_balanced_reference_grid(gpu, name):
+    print(f"balanced {name}", flush=True)
+    case = ref_case(GRID[name])
+    assert_close(balanced(case), numpy_oracle(case, SCALE), ATOL, RTOL, f"balanced/{name}")
+
+
+@pytest.mark.parametrize("nwg", [1, 2, 3, 7, 64, 256, 1000])
+def test_balanced_workgroup_counts(gpu, nwg):
+    # 1: one share, every piece whole, no merge launch; 1000 > the 96 tiles of
+    # the first case: most shares empty.
+    print(f"balanced nwg={nwg}", flush=True)
+    for cfg in (dict(S_list=[100, 257, 33, 1], Hq=32, Hkv=8, bs=16),
+                dict(S_list=[4000, 17, 900], Hq=16, Hkv=4, bs=16)):
+        case = ref_case(cfg, seed=nwg)
+        assert_close(balanced(case, nwg=nwg), numpy_oracle(case, SCALE), ATOL, RTOL, f"nwg{nwg}")
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 4])
+@pytest.mark.parametrize("bs", [1, 7, 16, 24, 64])
+def test_balanced_groups_and_block_sizes(gpu, G, bs):
+    print(f"balanced G={G} bs={bs}", flush=True)
+    cfg = dict(S_list=[1, 50, 333, 129, 700], Hq=4 * G, Hkv=4, bs=bs)
+    case = ref_case(cfg, seed=G * 100 + bs)
+    assert_close(balanced(case, nwg=37), numpy_oracle(case, SCALE), ATOL, RTOL, f"G{G}/bs{bs}")
+
+
+def test_balanced_zero_length_requests(gpu):
+    # seq_len 0 is unsupported (NaN, as in the reference); the other requests
+    # must be unaffected, whichever share the empty ones fall into.
+    S_list = [0, 37, 0, 0, 100, 0]
+    case = make_case(S_list, 32, 8, 16, pool_factor=2, seed=5, qkv_std=0.5, poison=True)
+    live = [i for i, s in enumerate(S_list) if s]
+    for nwg in (1, 2, 5, 256):
+        out = balanced(case, nwg=nwg).float().cpu()
+        assert torch.isnan(out[[i for i, s in enumerate(S_list) if not s]]).all()
+        assert_close(out[live].numpy(), oracle(case, SCALE, live), ATOL, RTOL, f"zero/nwg{nwg}")
+
+
+def test_balanced_many_requests(gpu):
+    # More requests than one 256-thread prefix-scan round, short and ragged.
+    g = np.random.default_rng(3)
+    S_list = [int(x) for x in g.integers(1, 300, size=700)]
+    case = make_case(S_list, 32, 8, 16, pool_factor=1.2, seed=6, qkv_std=0.5, poison=True)
+    out = balanced(case)
+    batches = list(range(0, 700, 7)) + [699]
+    assert_close(out[batches], oracle(case, SCALE, batches), ATOL, RTOL, "many")
+
+
+def test_balanced_repeatable(gpu):
+    cfg = dict(S_list=[5000, 1, 2000, 777, 3333, 64], Hq=32, Hkv=8, bs=16)
+    case = ref_case(cfg, seed=9)
+    first = balanced(case)
+    for _ in range(3):
+        assert torch.equal(balanced(case), first)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
+def test_balanced_configs(gpu, name):
+    # BASELINE configs with 4-head groups at full size, north_star tolerance.
+    print(f"balanced config {name}", flush=True)
+    case = make_config_case(name, seed=0, poison=(name == "c5"))
+    out = balanced(case)
+    assert torch.isfinite(out.float()).all()
+    B = case[0].shape[0]
+    if name == "c5":
+        S = config_seq_lens(name)
+        order = np.argsort(S)
+        batches = sorted({int(order[0]), int(order[-1]), 0, B - 1, B // 2, B // 3})
+    else:
+        batches = list(range(B))
+    assert_close(out[batches], oracle(case, SCALE, batches), 1e-2, 1e-2, f"balanced/{name}")
+    del case
+    torch.cuda.empty_cache()
+
+
+def test_balanced_parts_equal_launch(gpu):
+    # Partial then merge, as two calls, is the combined launch.
+    cfg = dict(S_list=[3000, 17, 900, 2500], Hq=32, Hkv=8, bs=16)
+    case = ref_case(cfg, seed=12)
+    assert torch.equal(balanced(case, parts=True), balanced(case))
+
+
+def test_balanced_ops(gpu):
+    # The op, and v2's automatic choice where the rule prefers the balanced
+    # launch, equal the C-ABI launch with one workgroup per CU bit for bit.
+    S_list = [int(x) for x in np.random.default_rng(4).integers(1, 32768, size=24)]
+    case = make_case(S_list, 32, 8, 16, pool_factor=1.1, seed=4, qkv_std=0.5)
+    q, k, v, bt, sl = case
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert prefer_balanced(q.shape[0], 32, 8, 16, bt.shape[1], cus)
+    want = balanced(case)
+    assert torch.equal(gqa_decode_balanced(*case, SCALE), want)
+    assert torch.equal(gqa_decode_v2(*case, SCALE, num_splits=0), want)
+    assert torch.equal(gqa_decode_balanced(*case, SCALE, num_workgroups=7), balanced(case, nwg=7))
+    with pytest.raises(RuntimeError, match="at most 4"):
+        gqa_decode_balanced(torch.zeros(1, 64, 128, dtype=torch.bfloat16, device=q.device), k, v,
+                            bt[:1], sl[:1], SCALE)
