@@ -173,10 +173,12 @@ GQA_DECODE_API int gqa_decode_balanced_merge_launch(
  * gqa_decode_pick_num_splits' count for this shape on num_cus CUs (<= 0: the
  * current device), else 0 (also for shapes the balanced launcher does not
  * serve). The rule, from measurements on MI355X: groups of at most 4 q-heads,
- * the split heuristic asking for more than one split, at least 64 MiB of KV
- * (B * max_blocks * block_size tokens), and at most 4 (request, kv-head)
- * segments per CU. This is the choice the torch op makes for num_splits=0.
- * Pure host code. No reference counterpart. */
+ * a longest sequence (max_blocks * block_size) of at least 6144 tokens, at
+ * least 32 MiB of KV (B * max_blocks * block_size tokens), at most 16
+ * (request, kv-head) segments per CU, and not a split grid of exactly one
+ * wave per SIMD with at most 8 splits (which uniform lengths make perfectly
+ * even). This is the choice the torch op makes for num_splits=0. Pure host
+ * code. No reference counterpart. */
 GQA_DECODE_API int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size,
                                               int max_blocks, int num_cus);
 

@@ -85,8 +85,11 @@ def sanity(cells, h100, bench):
         check(c["kv_bytes"] == b * s * 8 * KV_BYTES_PER_TOKEN_HEAD, f"{name}: kv_bytes formula")
         check(close(c["sol_ms"], c["kv_bytes"] / PEAK * 1e3), f"{name}: sol_ms at 8 TB/s")
         r = c["results"]
-        for k in ("v1", "v2", "v2_heuristic", c["baseline"]):
+        for k in ("v1", "v2", "v2_auto", c["baseline"]):
             check(k in r, f"{name}: result {k} present")
+        check(("balanced" in r) == (hq // 8 <= 4), f"{name}: balanced timed iff groups <= 4")
+        choice = r["v2_auto"]["choice"]
+        check(choice == "balanced" or isinstance(choice, int), f"{name}: automatic choice recorded")
         for k, v in r.items():
             check(close(v["pct_of_sol"], c["sol_ms"] / v["median_ms"] * 100),
                   f"{name}: {k} % of SoL = sol / median")
@@ -135,19 +138,26 @@ def sec_headline(bench, cells, h100):
     hr = h100[REP]
     lines += ["", f"Representative matrix cell (32x8, S=8192, B=32, block 16; the reference's "
               f"timing: events around each op call): v1 {us(c['v1']['median_ms'])} us, v2 best "
-              f"{us(c['v2']['median_ms'])} us (ns={c['v2']['best_splits']}), heuristic "
-              f"{us(c['v2_heuristic']['median_ms'])} us ({c['v2_heuristic']['pct_of_sol']:.1f} % "
-              f"of SoL). H100 reference: v2 best {us(float(hr['v2']['median_ms']))} us "
+              f"{us(c['v2']['median_ms'])} us (ns={c['v2']['best_splits']}), automatic choice "
+              f"{us(c['v2_auto']['median_ms'])} us ({choice_label(c['v2_auto'])}, "
+              f"{c['v2_auto']['pct_of_sol']:.1f} % of SoL). H100 reference: v2 best "
+              f"{us(float(hr['v2']['median_ms']))} us "
               f"(ns={hr['v2']['best_splits']}), FlashInfer {us(float(hr['flashinfer']['median_ms']))} us.",
               "", f"Source: {rel(BENCH_LINES)}, {rel(MATRIX_DIR)}, {rel(H100_CSV)}"]
     return lines
 
 
+def choice_label(r):
+    return "bal." if r["choice"] == "balanced" else f"ns={r['choice']}"
+
+
 def sec_pershape(cells, h100, block):
     lines = [f"## Per shape, block {block} (median us; x = speed-up)", "",
-             "| Hq/Hkv | S | B | v1 | v2 best (ns) | heuristic (ns) | % SoL | SDPA | x SDPA "
-             "| H100 v2 best | H100 FlashInfer | x H100 FlashInfer |",
-             "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+             "auto = v2 with num_splits=0 (bal. = the token-balanced launch, else the split "
+             "heuristic's count); % SoL is auto's.", "",
+             "| Hq/Hkv | S | B | v1 | v2 best (ns) | balanced | auto (choice) | % SoL | SDPA "
+             "| x SDPA | H100 v2 best | H100 FlashInfer | x H100 FlashInfer |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
     for hq in HEADTYPES:
         for s in S_LIST:
             for b in B_LIST:
@@ -155,48 +165,57 @@ def sec_pershape(cells, h100, block):
                 r = c["results"]
                 h = h100[(hq, s, b, block)]
                 base = r[c["baseline"]]["median_ms"]
-                heur = r["v2_heuristic"]["median_ms"]
+                auto = r["v2_auto"]["median_ms"]
                 fi = float(h["flashinfer"]["median_ms"])
+                bal = us(r["balanced"]["median_ms"]) if "balanced" in r else "-"
                 lines.append(
                     f"| {hq}/8 | {s} | {b} | {us(r['v1']['median_ms'])} | {us(r['v2']['median_ms'])} "
-                    f"({r['v2']['best_splits']}) | {us(heur)} ({r['v2_heuristic']['num_splits']}) "
-                    f"| {r['v2_heuristic']['pct_of_sol']:.1f} | {us(base)} | {base / heur:.2f} "
-                    f"| {us(float(h['v2']['median_ms']))} | {us(fi)} | {fi / heur:.2f} |")
+                    f"({r['v2']['best_splits']}) | {bal} | {us(auto)} ({choice_label(r['v2_auto'])}) "
+                    f"| {r['v2_auto']['pct_of_sol']:.1f} | {us(base)} | {base / auto:.2f} "
+                    f"| {us(float(h['v2']['median_ms']))} | {us(fi)} | {fi / auto:.2f} |")
     lines += ["", f"Source: {rel(MATRIX_DIR)}, {rel(H100_CSV)}"]
     return lines
 
 
+def best_ms(r):
+    """The best time any launch reached on the cell: the split sweep or the
+    token-balanced launch."""
+    return min(r["v2"]["median_ms"], r.get("balanced", r["v2"])["median_ms"])
+
+
 def sec_summary(cells):
-    heur_pct = [c["results"]["v2_heuristic"]["pct_of_sol"] for c in cells.values()]
-    regret = sorted((c["results"]["v2_heuristic"]["median_ms"] / c["results"]["v2"]["median_ms"], k)
+    heur_pct = [c["results"]["v2_auto"]["pct_of_sol"] for c in cells.values()]
+    regret = sorted((c["results"]["v2_auto"]["median_ms"] / best_ms(c["results"]), k)
                     for k, c in cells.items())
-    base = [(c["results"][c["baseline"]]["median_ms"] / c["results"]["v2_heuristic"]["median_ms"], k)
+    base = [(c["results"][c["baseline"]]["median_ms"] / c["results"]["v2_auto"]["median_ms"], k)
             for k, c in cells.items()]
+    nbal = sum(c["results"]["v2_auto"]["choice"] == "balanced" for c in cells.values())
     blk = []
     for (hq, s, b, bs), c in cells.items():
         if bs == 16:
             o = cells[(hq, s, b, 64)]
-            for k in ("v1", "v2_heuristic"):
+            for k in ("v1", "v2_auto"):
                 t16, t64 = c["results"][k]["median_ms"], o["results"][k]["median_ms"]
                 blk.append((abs(t16 - t64) / min(t16, t64) * 100, (hq, s, b), k))
-    sat = [c["results"]["v2_heuristic"]["pct_of_sol"] for (hq, s, b, bs), c in cells.items()
+    sat = [c["results"]["v2_auto"]["pct_of_sol"] for (hq, s, b, bs), c in cells.items()
            if c["kv_bytes"] >= 1 << 30]
 
     def name(k):
         return f"{k[0]}x8 S{k[1]} B{k[2]} bs{k[3]}"
 
     lines = ["## Summary over the 64 cells", "",
-             f"- Split heuristic vs the best of the sweep {{1,4,8,16,32,64}}: median ratio "
+             f"- Automatic choice (balanced in {nbal} cells, else the split heuristic) vs the best "
+             f"of the split sweep {{1,4,8,16,32,64}} and the balanced launch: median ratio "
              f"{statistics.median(x for x, _ in regret):.3f}, best {regret[0][0]:.3f} "
              f"({name(regret[0][1])}), worst {regret[-1][0]:.3f} ({name(regret[-1][1])}); "
-             f"{sum(x <= 1.0 for x, _ in regret)} of 64 cells at or below the sweep's best.",
-             f"- Heuristic % of 8 TB/s SoL: median {statistics.median(heur_pct):.1f}, max "
+             f"{sum(x <= 1.01 for x, _ in regret)} of 64 cells within 1 %.",
+             f"- Automatic choice, % of 8 TB/s SoL: median {statistics.median(heur_pct):.1f}, max "
              f"{max(heur_pct):.1f}; over the {len(sat)} cells with >= 1 GiB of KV: median "
              f"{statistics.median(sat):.1f}, min {min(sat):.1f}.",
              f"- Speed-up over the SDPA baseline: median {statistics.median(x for x, _ in base):.2f}x, "
              f"min {min(base)[0]:.2f}x ({name(min(base)[1])}), max {max(base)[0]:.2f}x "
              f"({name(max(base)[1])}).",
-             f"- Block size 16 vs 64 (v1 and heuristic v2, {len(blk)} pairs): median |difference| "
+             f"- Block size 16 vs 64 (v1 and automatic v2, {len(blk)} pairs): median |difference| "
              f"{statistics.median(x for x, _, _ in blk):.2f} %, {sum(x > 2 for x, _, _ in blk)} pairs "
              f"above 2 %.",
              "", f"Source: {rel(MATRIX_DIR)}"]
@@ -204,7 +223,7 @@ def sec_summary(cells):
 
 
 def sec_argbest(cells):
-    lines = ["## Best split count of the sweep (block 16)", "",
+    lines = ["## Best split count of the sweep (block 16; the automatic choice in brackets)", "",
              "| Hq/Hkv | S | " + " | ".join(f"B={b}" for b in B_LIST) + " |",
              "|---|---|" + "---|" * len(B_LIST)]
     for hq in HEADTYPES:
@@ -212,7 +231,7 @@ def sec_argbest(cells):
             row = []
             for b in B_LIST:
                 r = cells[(hq, s, b, 16)]["results"]
-                row.append(f"{r['v2']['best_splits']} (heur. {r['v2_heuristic']['num_splits']})")
+                row.append(f"{r['v2']['best_splits']} ({choice_label(r['v2_auto'])})")
             lines.append(f"| {hq}/8 | {s} | " + " | ".join(row) + " |")
     lines += ["", f"Source: {rel(MATRIX_DIR)}"]
     return lines

@@ -10,8 +10,10 @@ pool of 1.1x the needed blocks):
   fp32 torch reference (atol = rtol = 2e-2);
 * median time (HIP events around each call, bench/common.py:49-64 of the
   reference) of the baseline's run() only, v1, v2 at num_splits
-  {1,4,8,16,32,64} (best recorded) and at the split heuristic (num_splits=0),
-  and v0 where it is not prohibitively slow (S <= 2048 and B <= 8);
+  {1,4,8,16,32,64} (best recorded), v2's automatic choice (num_splits=0: the
+  token-balanced launch or the split heuristic's count, recorded), the
+  token-balanced launch itself (groups of at most 4 q-heads), and v0 where it
+  is not prohibitively slow (S <= 2048 and B <= 8);
 * 0.5 s of untimed calls (steady clocks), then each variant timed as the
   reference times it -- 10 warmup calls, 50 timed (30 for S=32768, B>=32),
   events around each call, synchronize after each -- in two passes over the
@@ -43,7 +45,8 @@ sys.path.insert(0, _HERE)
 sys.path.insert(0, os.path.join(os.path.dirname(_HERE), "python"))
 
 import cases  # noqa: E402
-from binding import KERNELS, gqa_decode_v2, num_splits_heuristic  # noqa: E402
+from binding import (KERNELS, gqa_decode_balanced, gqa_decode_v2,  # noqa: E402
+                     num_splits_heuristic, prefer_balanced)
 
 HEADTYPES = [(32, 8), (64, 8)]
 S_LIST = [512, 2048, 8192, 32768]
@@ -99,9 +102,14 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
     checks = {"v1": cases.spot_check(KERNELS["v1"], case, scale, label="v1")}
 
     warmup, runs = (10, 30) if (S == 32768 and B >= 32) else (10, 50)
-    h = num_splits_heuristic(B, Hq, Hkv, bs, case[3].shape[1], num_cus)
-    checks["v2_heuristic"] = cases.spot_check(
-        lambda *a: gqa_decode_v2(*a, num_splits=0), case, scale, label="v2 heuristic")
+    mb = case[3].shape[1]
+    choice = ("balanced" if prefer_balanced(B, Hq, Hkv, bs, mb, num_cus)
+              else num_splits_heuristic(B, Hq, Hkv, bs, mb, num_cus))
+    checks["v2_auto"] = cases.spot_check(
+        lambda *a: gqa_decode_v2(*a, num_splits=0), case, scale, label="v2 automatic")
+    with_balanced = Hq // Hkv <= 4
+    if with_balanced:
+        checks["balanced"] = cases.spot_check(gqa_decode_balanced, case, scale, label="balanced")
 
     fns = {}
     if baseline != "none":
@@ -111,12 +119,14 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
     fns["v1"] = lambda: KERNELS["v1"](*case, scale)
     for ns in SPLITS_LIST:
         fns[f"v2/{ns}"] = (lambda n: lambda: gqa_decode_v2(*case, scale, num_splits=n))(ns)
-    fns["v2_heuristic"] = lambda: gqa_decode_v2(*case, scale, num_splits=0)
+    fns["v2_auto"] = lambda: gqa_decode_v2(*case, scale, num_splits=0)
+    if with_balanced:
+        fns["balanced"] = lambda: gqa_decode_balanced(*case, scale)
     if S <= 2048 and B <= 8:
         fns["v0"] = lambda: KERNELS["v0"](*case, scale)
 
     # Clocks drop while the host builds the case; bring them back up first.
-    ramp(fns["v2_heuristic"], RAMP_SECONDS)
+    ramp(fns["v2_auto"], RAMP_SECONDS)
     ms = cases.time_ops_two_pass(fns, warmup, runs)
 
     def entry(t, **extra):
@@ -129,7 +139,9 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
     by_splits = {ns: ms[f"v2/{ns}"] for ns in SPLITS_LIST}
     best = min(by_splits, key=by_splits.get)
     results["v2"] = entry(by_splits[best], by_splits=by_splits, best_splits=best)
-    results["v2_heuristic"] = entry(ms["v2_heuristic"], num_splits=h)
+    results["v2_auto"] = entry(ms["v2_auto"], choice=choice)
+    if with_balanced:
+        results["balanced"] = entry(ms["balanced"])
     if "v0" in ms:
         results["v0"] = entry(ms["v0"])
 
@@ -158,7 +170,7 @@ def write_summary(out_dir):
                 "headtype": f"{cell['Hq']}x{cell['Hkv']}",
                 "S": cell["S"], "B": cell["B"], "block": cell["block"],
                 "kernel": kernel,
-                "num_splits": r.get("best_splits", r.get("num_splits", "")),
+                "num_splits": r.get("best_splits", r.get("choice", "")),
                 "median_ms": r["median_ms"],
                 "pct_of_sol": r["pct_of_sol"],
                 # > 1: faster than the baseline
@@ -214,9 +226,9 @@ def main(argv=None):
         base = f" {args.baseline} {r[args.baseline]['median_ms'] * 1e3:.1f} us" \
             if args.baseline in r else ""
         print(f"[{i}/{len(cells)}] {name}: done in {dt:.1f}s; v2 best "
-              f"{r['v2']['median_ms'] * 1e3:.1f} us (ns={r['v2']['best_splits']}), heuristic "
-              f"{r['v2_heuristic']['median_ms'] * 1e3:.1f} us "
-              f"({r['v2_heuristic']['pct_of_sol']:.1f}% SoL){base}; "
+              f"{r['v2']['median_ms'] * 1e3:.1f} us (ns={r['v2']['best_splits']}), automatic "
+              f"{r['v2_auto']['median_ms'] * 1e3:.1f} us ({r['v2_auto']['choice']}, "
+              f"{r['v2_auto']['pct_of_sol']:.1f}% SoL){base}; "
               f"~{(len(cells) - i) * sum(durations) / len(durations) / 60:.1f} min left",
               flush=True)
 

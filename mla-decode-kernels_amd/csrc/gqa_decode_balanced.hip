@@ -435,24 +435,31 @@ extern "C" int gqa_decode_balanced_merge_launch(
 
 extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size, int max_blocks,
                                           int num_cus) {
-  // Measured on MI355X: the token-balanced launch wins where per-request splits
-  // are uneven (ragged lengths, or a split count the length bound forces on a
-  // grid that was already full) and costs a few microseconds of fixed
-  // overhead (prefix sums, a second launch) where they are even. It is
-  // preferred when the split heuristic would split at all (one split means
-  // the grid already holds exactly one round of whole segments), the batch
-  // holds at least kMinBytes of KV (so the overhead stays small), and there
-  // are at most kMaxSegmentsPerCu segments per workgroup (each piece restarts
-  // the load pipeline).
-  constexpr int64_t kMinBytes = int64_t(64) << 20;
-  constexpr int kMaxSegmentsPerCu = 4;
+  // Measured on MI355X over the 64-cell matrix and ragged batches: the
+  // token-balanced launch wins where the split-rule grid is uneven -- ragged
+  // lengths, or more waves than one per SIMD (a grid the split heuristic could
+  // not make exactly one round) -- and where many splits make the split merge
+  // heavy, as long as segments are long enough that restarting the load
+  // pipeline at each piece stays cheap. It loses a few percent where the split
+  // grid is exactly one round of one wave per SIMD with few splits (uniform
+  // lengths make that perfect) and on short or small batches.
+  // Preferred when: groups of at most 4 q-heads, sequences up to at least
+  // kMinLongest tokens, at least kMinBytes of KV, at most kMaxSegmentsPerCu
+  // segments per CU, and a split grid that is not exactly one round of at
+  // most kMaxEvenSplits splits.
+  constexpr int64_t kMinLongest = 6144;
+  constexpr int64_t kMinBytes = int64_t(32) << 20;
+  constexpr int kMaxSegmentsPerCu = 16;
+  constexpr int kMaxEvenSplits = 8;
   if (num_cus <= 0 && (num_cus = gqa::device_cu_count()) <= 0) return 0;
   if (B < 1 || Hkv < 1 || Hq % Hkv != 0 || Hq / Hkv > GQA_DECODE_BALANCED_MAX_GROUP ||
       B > gqa::kBalancedMaxB || block_size < 1 || max_blocks < 1)
     return 0;
   const int64_t s_cap = (int64_t)max_blocks * block_size;
   if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31)) return 0;
-  if (gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus) <= 1) return 0;
-  if ((int64_t)B * s_cap * Hkv * gqa::kHeadDim * 4 < kMinBytes) return 0;
-  return (int64_t)B * Hkv <= (int64_t)kMaxSegmentsPerCu * num_cus ? 1 : 0;
+  if (s_cap < kMinLongest || (int64_t)B * s_cap * Hkv * gqa::kHeadDim * 4 < kMinBytes) return 0;
+  if ((int64_t)B * Hkv > (int64_t)kMaxSegmentsPerCu * num_cus) return 0;
+  const int ns = gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus);
+  const int64_t split_waves = (int64_t)B * Hkv * gqa::kWavesPerHead * ns;
+  return split_waves == (int64_t)num_cus * 4 && ns <= kMaxEvenSplits ? 0 : 1;
 }

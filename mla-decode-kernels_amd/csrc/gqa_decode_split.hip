@@ -120,31 +120,46 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs 
 
 // Log-sum-exp merge of the num_splits states of each (b, q-head) in split order
 // (v2_splitkv.cu:92-108): one wave per (b, q-head), lane i owns dims 2i, 2i+1.
+// The lanes find the max together (one split each), then the splits are folded
+// in order, their states loaded kBatch at a time so the loads overlap.
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(const float* __restrict__ ws_acc,
                                                                const float* __restrict__ ws_m,
                                                                const float* __restrict__ ws_l,
                                                                uint16_t* __restrict__ out, int BH,
                                                                int ns) {
+  constexpr int kBatch = 8;
   const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (bh >= BH) return;
   const size_t st0 = (size_t)bh * ns;
-  float M = kNegInf;
-  for (int i = 0; i < ns; ++i) M = fmaxf(M, ws_m[st0 + i]);
+  float mloc = kNegInf;
+  for (int i = lane; i < ns; i += 64) mloc = fmaxf(mloc, ws_m[st0 + i]);
+  const float M = wave_max(mloc);
   float L = 0.f, A0 = 0.f, A1 = 0.f;
-  for (int i = 0; i < ns; ++i) {
-    const float mi = ws_m[st0 + i];
-    // Exactly 1 for the split holding the max, so one split is a no-op merge.
-    const float f = mi == M ? 1.f : exp2_fast((mi - M) * kLog2e);
-    const float2 av = reinterpret_cast<const float2*>(ws_acc + (st0 + i) * kHeadDim)[lane];
-    if (i == 0) {
-      L = ws_l[st0] * f;
-      A0 = av.x * f;
-      A1 = av.y * f;
-    } else {
-      L = fmaf(ws_l[st0 + i], f, L);
-      A0 = fmaf(av.x, f, A0);
-      A1 = fmaf(av.y, f, A1);
+  for (int i0 = 0; i0 < ns; i0 += kBatch) {
+    float mi[kBatch], li[kBatch];
+    float2 av[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const size_t st = st0 + min(i0 + k, ns - 1);  // past the end: a valid split, not folded
+      mi[k] = ws_m[st];
+      li[k] = ws_l[st];
+      av[k] = reinterpret_cast<const float2*>(ws_acc + st * kHeadDim)[lane];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (i0 + k >= ns) break;
+      // Exactly 1 for the split holding the max, so one split is a no-op merge.
+      const float f = mi[k] == M ? 1.f : exp2_fast((mi[k] - M) * kLog2e);
+      if (i0 + k == 0) {
+        L = li[k] * f;
+        A0 = av[k].x * f;
+        A1 = av[k].y * f;
+      } else {
+        L = fmaf(li[k], f, L);
+        A0 = fmaf(av[k].x, f, A0);
+        A1 = fmaf(av[k].y, f, A1);
+      }
     }
   }
   const uint32_t lo = f32_to_bf16_bits(finalize(A0, L));

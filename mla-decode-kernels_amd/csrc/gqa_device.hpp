@@ -61,6 +61,17 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Max over all 64 lanes, identical in every lane (max is exact, so the order
+// of the steps does not matter).
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));
+  x = fmaxf(x, dpp_f32<0x4E>(x));
+  x = fmaxf(x, dpp_f32<0x141>(x));
+  x = fmaxf(x, dpp_f32<0x140>(x));
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+
 // Hardware 2^x (v_exp_f32): 2^-inf = 0, 2^0 = 1.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -198,23 +198,27 @@ def test_balanced_parts_reject_bad_arguments(fn, over):
 
 
 def test_prefer_balanced_headline_shapes():
-    # BASELINE configs 1..5 on 256 CUs: balanced for the long/ragged 4-head
-    # configs (3, 5); the split path where one split already fills the chip
-    # (2), for 8-head groups (4) and for tiny batches (1).
+    # BASELINE configs 1..5 on 256 CUs: balanced for the ragged config (5);
+    # the split path where the split grid is exactly one wave per SIMD (2, 3),
+    # for 8-head groups (4) and for tiny batches (1).
     shapes = [(1, 32, 16, 32), (32, 32, 16, 512), (8, 32, 64, 512), (32, 64, 64, 512),
               (128, 32, 16, 2048)]
     assert [capi.prefer_balanced(B, Hq, 8, bs, mb, 256) for B, Hq, bs, mb in shapes] == \
-        [0, 0, 1, 0, 1]
+        [0, 0, 0, 0, 1]
 
 
 @pytest.mark.parametrize("B,Hq,bs,mb", [(1, 32, 16, 2048), (8, 32, 16, 512), (32, 32, 64, 512),
                                         (128, 32, 16, 2048), (256, 32, 16, 2048), (1, 32, 16, 64),
-                                        (4, 16, 16, 4096), (2, 64, 16, 4096)])
+                                        (4, 16, 16, 4096), (2, 64, 16, 4096), (128, 32, 16, 512),
+                                        (64, 32, 16, 512), (600, 32, 16, 1024), (3, 24, 16, 2048),
+                                        (1, 32, 16, 512), (128, 32, 16, 511), (512, 32, 16, 256)])
 def test_prefer_balanced_rule(B, Hq, bs, mb):
     # The documented rule, clause by clause.
     Hkv, cus = 8, 256
-    want = (Hq // Hkv <= 4 and capi.pick_num_splits(B, Hq, Hkv, bs, mb, cus) > 1
-            and B * mb * bs * Hkv * 512 >= 64 << 20 and B * Hkv <= 4 * cus)
+    s_max = mb * bs
+    ns = capi.pick_num_splits(B, Hq, Hkv, bs, mb, cus)
+    want = (Hq // Hkv <= 4 and s_max >= 6144 and B * s_max * Hkv * 512 >= 32 << 20
+            and B * Hkv <= 16 * cus and not (B * Hkv * 4 * ns == 4 * cus and ns <= 8))
     assert capi.prefer_balanced(B, Hq, Hkv, bs, mb, cus) == int(want)
 
 
