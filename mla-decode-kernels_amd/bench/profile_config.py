@@ -1,0 +1,205 @@
+"""rocprofv3 passes over one bench.py configuration, and their summary.
+
+The MI355X counterpart of the reference's analysis/ncu/run_ncu.sh and
+extract.py (Nsight Compute sections reduced to DRAM bytes, L2 hit,
+occupancy, stalls): one rocprofv3 run per pass, each under its own time limit,
+then a reduction of the CSV output to per-kernel durations, per-kernel
+counter means and the HBM traffic of the dominant kernel, calibrated by the
+same counters on a plain 1 GiB copy (bench.py --copy-probe 1024).
+
+    python profile_config.py --config c5 --out-dir <dir>          # run + summarize
+    python profile_config.py --summarize <dir> [--config c5]      # summarize only
+
+Passes (each counter set within one rocprofv3 pass's hardware limits):
+  trace   --kernel-trace --stats over a 50-step bench run
+  fetch   FETCH_SIZE                     write   WRITE_SIZE
+  occ     SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_VALU_MFMA_BUSY_CYCLES
+          SQ_WAIT_INST_ANY SQ_INSTS_VALU SQ_INSTS_MFMA GRBM_GUI_ACTIVE
+  lds     SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS SQ_WAVES SQ_INSTS_VMEM_RD
+          GRBM_GUI_ACTIVE
+  l2      TCC_HIT_sum TCC_MISS_sum
+  copy_fetch / copy_write   the copy calibration (FETCH_SIZE / WRITE_SIZE)
+This script never touches the GPU itself: rocprofv3 starts bench.py as its
+program (after `--`), one child process per pass.
+"""
+
+import argparse
+import csv
+import glob
+import json
+import os
+import re
+import statistics
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO_ROOT = os.path.dirname(os.path.dirname(HERE))
+BENCH = os.path.join(REPO_ROOT, "bench.py")
+COPY_BYTES = 1 << 30
+
+PASSES = {
+    "trace": ["--kernel-trace", "--stats"],
+    "fetch": ["--pmc", "FETCH_SIZE"],
+    "write": ["--pmc", "WRITE_SIZE"],
+    "occ": ["--pmc", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_ACTIVE_INST_VALU",
+            "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_WAIT_INST_ANY", "SQ_INSTS_VALU", "SQ_INSTS_MFMA",
+            "GRBM_GUI_ACTIVE"],
+    "lds": ["--pmc", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_WAVES",
+            "SQ_INSTS_VMEM_RD", "GRBM_GUI_ACTIVE"],
+    "l2": ["--pmc", "TCC_HIT_sum", "TCC_MISS_sum"],
+    "copy_fetch": ["--pmc", "FETCH_SIZE"],
+    "copy_write": ["--pmc", "WRITE_SIZE"],
+}
+SHORT_RUN = ["--steps", "3", "--warmup", "1", "--ramp-seconds", "0", "--no-cpu-baseline"]
+
+
+def bench_args(pass_name, config):
+    if pass_name.startswith("copy_"):
+        return ["--copy-probe", "1024"]
+    if pass_name == "trace":
+        return ["--config", config, "--steps", "50", "--no-cpu-baseline"]
+    return ["--config", config] + SHORT_RUN
+
+
+def command(pass_name, config, out_dir):
+    return (["rocprofv3", "-f", "csv"] + PASSES[pass_name] +
+            ["-d", os.path.join(out_dir, pass_name), "-o", "run", "--", sys.executable, BENCH] +
+            bench_args(pass_name, config))
+
+
+def run_passes(config, out_dir, passes, timeout):
+    os.makedirs(out_dir, exist_ok=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    for name in passes:
+        cmd = command(name, config, out_dir)
+        print("==", name, " ".join(cmd), flush=True)
+        with open(os.path.join(out_dir, f"{name}.log"), "w") as log:
+            # A pass that asks for more counters than the hardware holds hangs
+            # instead of failing; the limit ends it (and the script).
+            proc = subprocess.run(cmd, cwd="/tmp", env=env, stdout=log, stderr=subprocess.STDOUT,
+                                  timeout=timeout)
+        if proc.returncode != 0:
+            raise SystemExit(f"pass {name} failed with status {proc.returncode}")
+        for db in glob.glob(os.path.join(out_dir, name, "**", "*.db"), recursive=True):
+            os.remove(db)  # raw databases stay out of the summary folder
+
+
+# ------------------------------------------------------------------ summary
+
+def short_name(name):
+    """Kernel name without its argument list and 'void ' prefix."""
+    return re.sub(r"\(.*", "", name).replace("void ", "").strip()
+
+
+def read_csvs(directory, suffix):
+    rows = []
+    for f in sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True)):
+        with open(f) as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def kernel_durations(directory, pattern="gqa"):
+    """{kernel: [durations in us]} from a --kernel-trace pass."""
+    out = {}
+    for r in read_csvs(directory, "kernel_trace.csv"):
+        name = r.get("Kernel_Name", "")
+        if re.search(pattern, name):
+            dt = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            out.setdefault(short_name(name), []).append(dt)
+    return out
+
+
+def counter_means(directory, pattern="gqa|neg_kernel"):
+    """{(kernel, counter): mean value over dispatches} from a --pmc pass."""
+    acc = {}
+    for r in read_csvs(directory, "counter_collection.csv"):
+        name = r.get("Kernel_Name", "")
+        if re.search(pattern, name):
+            acc.setdefault((short_name(name), r["Counter_Name"]), []).append(
+                float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def calibration(root):
+    """Bytes per counter unit for FETCH_SIZE and WRITE_SIZE: the copy of
+    COPY_BYTES read and written, over what each counter reported for it."""
+    f = {k: v for k, v in counter_means(os.path.join(root, "copy_fetch"), "neg_kernel").items()
+         if k[1] == "FETCH_SIZE"}
+    w = {k: v for k, v in counter_means(os.path.join(root, "copy_write"), "neg_kernel").items()
+         if k[1] == "WRITE_SIZE"}
+    if len(f) != 1 or len(w) != 1:
+        return None
+    return COPY_BYTES / next(iter(f.values())), COPY_BYTES / next(iter(w.values()))
+
+
+def summarize(root):
+    lines = []
+    dur = kernel_durations(os.path.join(root, "trace"))
+    lines.append("| kernel | calls | average | median | min | max | std dev |")
+    lines.append("|---|---|---|---|---|---|---|")
+    for name, v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        v = sorted(v)
+        sd = statistics.pstdev(v) if len(v) > 1 else 0.0
+        lines.append(f"| {name} | {len(v)} | {sum(v) / len(v):.2f} us | {v[len(v) // 2]:.2f} us "
+                     f"| {v[0]:.2f} us | {v[-1]:.2f} us | {sd:.2f} us |")
+    counters = {}
+    for p in ("fetch", "write", "occ", "lds", "l2"):
+        counters.update(counter_means(os.path.join(root, p)))
+    lines += ["", "| kernel | counter | mean per dispatch |", "|---|---|---|"]
+    for (k, c), v in sorted(counters.items()):
+        lines.append(f"| {k} | {c} | {v:,.0f} |")
+    cal = calibration(root)
+    traffic = None
+    if cal and dur:
+        dominant = max(dur, key=lambda k: sum(dur[k]))
+        fetch = counters.get((dominant, "FETCH_SIZE"))
+        write = counters.get((dominant, "WRITE_SIZE"))
+        if fetch is not None and write is not None:
+            traffic = (round(fetch * cal[0]), round(write * cal[1]))
+            lines += ["", f"Calibration: FETCH_SIZE x {cal[0]:.1f} B, WRITE_SIZE x {cal[1]:.1f} B "
+                      f"per unit (copy of {COPY_BYTES} B).",
+                      f"Dominant kernel {dominant}: fetch {traffic[0]:,} B, write {traffic[1]:,} B "
+                      "per dispatch."]
+    return "\n".join(lines), traffic
+
+
+def traffic_line(root, config, traffic):
+    """The profiles/traffic.txt line for this run: config, kernel label and
+    split label as bench.py records them, then the calibrated bytes."""
+    out = glob.glob(os.path.join(root, "trace.log"))
+    split = None
+    for f in out:
+        for line in open(f):
+            if line.startswith("{") and '"metric"' in line:
+                split = json.loads(line)["config"]["num_splits"]
+    kernel = "v2"
+    return f"{config} {kernel} {split} {traffic[0]} {traffic[1]}" if split is not None else None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--out-dir", default=None)
+    ap.add_argument("--passes", default=",".join(PASSES))
+    ap.add_argument("--timeout", type=int, default=300, help="seconds per pass")
+    ap.add_argument("--summarize", default=None, help="only summarize an existing output dir")
+    args = ap.parse_args(argv)
+    root = args.summarize or args.out_dir
+    if root is None:
+        ap.error("give --out-dir (run and summarize) or --summarize <dir>")
+    if not args.summarize:
+        run_passes(args.config, root, [p for p in args.passes.split(",") if p], args.timeout)
+    text, traffic = summarize(root)
+    with open(os.path.join(root, "summary.md"), "w") as f:
+        f.write(text + "\n")
+    print(text)
+    if traffic:
+        line = traffic_line(root, args.config, traffic)
+        if line:
+            print("traffic line:", line)
+
+
+if __name__ == "__main__":
+    main()

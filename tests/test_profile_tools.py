@@ -1,0 +1,74 @@
+"""The rocprofv3 pass runner and its summary (CPU: command shapes and the
+reduction of synthetic rocprofv3 CSV output)."""
+
+import csv
+import json
+import os
+
+import pytest
+
+import profile_config as pc
+
+# Per-pass hardware limits of one rocprofv3 --pmc run on this GPU, in counter
+# units (FETCH_SIZE takes 3 TCC units, WRITE_SIZE 2).
+TCC_UNITS = {"FETCH_SIZE": 3, "WRITE_SIZE": 2, "TCC_HIT_sum": 1, "TCC_MISS_sum": 1}
+
+
+@pytest.mark.parametrize("name", list(pc.PASSES))
+def test_pass_commands(name):
+    cmd = pc.command(name, "c5", "/tmp/x")
+    # The program follows "--" directly (no env/sh/launcher in between).
+    i = cmd.index("--")
+    assert cmd[i + 1].endswith("python") or "python" in os.path.basename(cmd[i + 1])
+    assert cmd[i + 2].endswith("bench.py")
+    opts = pc.PASSES[name]
+    if "--pmc" in opts:
+        assert not {"--kernel-trace", "--sys-trace", "-s", "--runtime-trace", "-r"} & set(opts)
+        counters = opts[opts.index("--pmc") + 1:]
+        assert sum(c.startswith("SQ_") for c in counters) <= 8
+        assert sum(TCC_UNITS.get(c, 0) for c in counters if c in TCC_UNITS) <= 4
+        assert sum(c.startswith("GRBM_") for c in counters) <= 2
+    if name.startswith("copy_"):
+        assert cmd[-2:] == ["--copy-probe", "1024"]
+    else:
+        assert cmd[cmd.index("--config") + 1] == "c5"
+
+
+def write_csv(path, rows):
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_summarize(tmp_path):
+    root = str(tmp_path)
+    scan = "void gqa::gqa_decode_balanced_kernel<4, 4, 2, true>(gqa::ScanArgs, gqa::BalancedArgs)"
+    merge = "void gqa::gqa_decode_balanced_merge_kernel<4, 4>(gqa::ScanArgs, gqa::BalancedArgs)"
+    trace = [dict(Kernel_Name=scan, Start_Timestamp=0, End_Timestamp=1_000_000),
+             dict(Kernel_Name=scan, Start_Timestamp=0, End_Timestamp=1_200_000),
+             dict(Kernel_Name=scan, Start_Timestamp=0, End_Timestamp=1_100_000),
+             dict(Kernel_Name=merge, Start_Timestamp=0, End_Timestamp=5_000),
+             dict(Kernel_Name="void other_kernel()", Start_Timestamp=0, End_Timestamp=9)]
+    write_csv(os.path.join(root, "trace", "x", "run_kernel_trace.csv"), trace)
+
+    def counters(pass_name, kernel, name, values):
+        write_csv(os.path.join(root, pass_name, "x", "run_counter_collection.csv"),
+                  [dict(Kernel_Name=kernel, Counter_Name=name, Counter_Value=v) for v in values])
+
+    neg = "void at::native::vectorized_elementwise_kernel<4, at::native::neg_kernel_cuda(...)"
+    counters("copy_fetch", neg, "FETCH_SIZE", [524288, 524288])   # KiB-like units
+    counters("copy_write", neg, "WRITE_SIZE", [1048576])
+    counters("fetch", scan, "FETCH_SIZE", [1000, 1002])
+    counters("write", scan, "WRITE_SIZE", [8])
+    with open(os.path.join(root, "trace.log"), "w") as f:
+        f.write("progress line\n" + json.dumps({"metric": "m", "config": {"num_splits": "balanced"}})
+                + "\n")
+
+    text, traffic = pc.summarize(root)
+    assert "gqa::gqa_decode_balanced_kernel<4, 4, 2, true> | 3 | 1100.00 us | 1100.00 us" in text
+    assert "other_kernel" not in text
+    # 2^30 bytes per 524288 units = 2048 B per FETCH unit, 1024 per WRITE unit.
+    assert traffic == (1001 * 2048, 8 * 1024)
+    assert pc.traffic_line(root, "c5", traffic) == f"c5 v2 balanced {1001 * 2048} {8 * 1024}"
