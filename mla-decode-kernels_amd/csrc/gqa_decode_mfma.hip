@@ -148,13 +148,11 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_mfma_kernel(const ScanArgs 
         const uint32_t sk = ts + 16 * tg + j < seg_end ? slot0 + j : slot0;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          t.k[tg][kk] = *reinterpret_cast<const uint4*>(a.k_cache + blk + sk * row_elems +
-                                                        32 * kk + 8 * g);
+          t.k[tg][kk] = load_kv(a.k_cache + blk + sk * row_elems + 32 * kk + 8 * g);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t sv = ts + 16 * tg + 4 * i + g < seg_end ? slot0 + 4 * i + g : slot0;
-          t.v[4 * tg + i] = *reinterpret_cast<const uint4*>(a.v_cache + blk + sv * row_elems +
-                                                            8 * j);
+          t.v[4 * tg + i] = load_kv(a.v_cache + blk + sv * row_elems + 8 * j);
         }
       }
     } else {
@@ -165,13 +163,13 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_mfma_kernel(const ScanArgs 
         const size_t rk = row_of(tk);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          t.k[tg][kk] = *reinterpret_cast<const uint4*>(a.k_cache + rk + 32 * kk + 8 * g);
+          t.k[tg][kk] = load_kv(a.k_cache + rk + 32 * kk + 8 * g);
       }
 #pragma unroll
       for (int i = 0; i < 4 * NG; ++i) {
         int tv = ts + 4 * i + g;
         tv = tv < seg_end ? tv : ts;
-        t.v[i] = *reinterpret_cast<const uint4*>(a.v_cache + row_of(tv) + 8 * j);
+        t.v[i] = load_kv(a.v_cache + row_of(tv) + 8 * j);
       }
     }
   };

@@ -109,8 +109,8 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
         const int tok = ts + 4 * j + r;
         const uint32_t slot = tok < seg_end ? slot0 + 4 * j + r : slot0;
         const uint32_t off = slot * row_elems + 8 * c;
-        t.k[j] = *reinterpret_cast<const uint4*>(kblk + off);
-        t.v[j] = *reinterpret_cast<const uint4*>(vblk + off);
+        t.k[j] = load_kv(kblk + off);
+        t.v[j] = load_kv(vblk + off);
       }
     } else {
 #pragma unroll
@@ -120,8 +120,8 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
         const uint32_t lb = fastdiv((uint32_t)tok, a.bs_div);
         const int slot = tok - (int)lb * bs;
         const size_t off = ((size_t)bt[lb] * bs + slot) * row_elems;
-        t.k[j] = *reinterpret_cast<const uint4*>(kbase + off);
-        t.v[j] = *reinterpret_cast<const uint4*>(vbase + off);
+        t.k[j] = load_kv(kbase + off);
+        t.v[j] = load_kv(vbase + off);
       }
     }
   };
