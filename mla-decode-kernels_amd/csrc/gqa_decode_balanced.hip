@@ -172,8 +172,9 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_balanced_kernel(const ScanA
     load_q(a, b, h0, G, c, qf);
     WaveState<GH> st;
     init_state(st);
-    scan_segment<GH, P, DEPTH, kBlockUniform>(a, a.block_table + (size_t)b * a.max_blocks, hkv,
-                                              qf, kTile * lt0, min(S, kTile * lt1), ph, r, c, st);
+    scan_segment<GH, P, DEPTH, kBlockUniform, true>(a, a.block_table + (size_t)b * a.max_blocks,
+                                                    hkv, qf, kTile * lt0, min(S, kTile * lt1), ph,
+                                                    r, c, st);
     float Mw[GH], Lw[GH];
     merge_rows(st, Mw, Lw);
     __syncthreads();  // the previous piece's reads of lds are done

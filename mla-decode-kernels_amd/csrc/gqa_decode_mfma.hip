@@ -120,6 +120,12 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_mfma_kernel(const ScanArgs 
 
   const uint32_t row_elems = (uint32_t)a.Hkv * kHeadDim;
   const int* bt = a.block_table + (size_t)b * a.max_blocks;
+  // The table is read-only for the launch. Reading it through the constant
+  // address space makes the uniform block-id load scalar: as a vector load it
+  // would share vmcnt with the tile loads, and waiting for it would drain every
+  // load in flight (measured: 2-3% on 64Q/8KV, S=32768).
+  const __attribute__((address_space(4))) int* btc =
+      (const __attribute__((address_space(4))) int*)bt;
   const int bs = a.block_size;
   const size_t head_off = (size_t)hkv * kHeadDim;
 
@@ -144,7 +150,7 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_mfma_kernel(const ScanArgs 
         const int tb = ts + 16 * tg < seg_end ? ts + 16 * tg : ts;
         const uint32_t lb = fastdiv((uint32_t)tb, a.bs_div);
         const uint32_t slot0 = (uint32_t)(tb - (int)lb * bs);
-        const size_t blk = (size_t)bt[lb] * ((size_t)bs * row_elems) + head_off;
+        const size_t blk = (size_t)btc[lb] * ((size_t)bs * row_elems) + head_off;
         const uint32_t sk = ts + 16 * tg + j < seg_end ? slot0 + j : slot0;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)

@@ -73,7 +73,13 @@ __device__ __forceinline__ void load_q(const ScanArgs& a, int b, int h0, int nh,
 // folds them into st. DEPTH register tiles are in flight; the steady-state
 // loop issues tile k + DEPTH - 1 before consuming tile k and has no branch, so
 // the wait before each consume covers only the tile being consumed.
-template <int GH, int P, int DEPTH, bool kBlockUniform>
+// kPinIssue puts a scheduling barrier after each tile's loads: without it the
+// compiler may sink a tile's loads below the previous tile's arithmetic, so
+// that tile is consumed right after its loads are issued. Measured on MI355X:
+// pinning speeds the token-balanced kernel up ~5% (ragged B=128 batch) and is
+// neutral to 1% slower for the split-rule kernel, whose default schedule
+// already overlaps.
+template <int GH, int P, int DEPTH, bool kBlockUniform, bool kPinIssue = false>
 __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, int hkv,
                                              const uint4 (&qf)[GH], int seg_start, int seg_end,
                                              int ph, int r, int c, WaveState<GH>& st) {
@@ -177,6 +183,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
 #pragma unroll
       for (int i = 0; i < DEPTH; ++i) {
         issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
+        if constexpr (kPinIssue) __builtin_amdgcn_sched_barrier(0);
         consume(k + i, t[i]);
       }
     }
@@ -184,6 +191,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
     for (int i = 0; i < DEPTH; ++i) {
       if (k + i < my_tiles) {
         if (k + i + DEPTH - 1 < my_tiles) issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
+        if constexpr (kPinIssue) __builtin_amdgcn_sched_barrier(0);
         consume(k + i, t[i]);
       }
     }
