@@ -42,6 +42,18 @@ __device__ __forceinline__ uint4 load_kv(const uint16_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// The same streaming load through a raw buffer resource: a uniform base in
+// SGPRs plus a 32-bit per-lane byte offset, so no 64-bit address arithmetic
+// per load. kv_rsrc(base) covers [base, base + 4 GiB) (stride 0; the last
+// descriptor word is the gfx9-family raw-buffer format); cache-policy value 2
+// sets nt.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ uint4 load_kv(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_off, 0, 2));
+}
+
 // acc += <a, b> over two packed bf16 pairs (v_dot2c_f32_bf16).
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),

@@ -14,6 +14,8 @@
 // consumed.
 #pragma once
 
+#include <type_traits>
+
 #include "gqa_device.hpp"
 #include "gqa_scan.hpp"
 
@@ -97,26 +99,35 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
 
   auto tile_start = [&](int k) { return seg_start + kTile * (ph + P * k); };
 
+  // Per-lane byte offsets of the tile's K/V loads from its first slot's
+  // kv-head row: load j reads token 4j + r, dims [8c, 8c + 8). A block's
+  // bytes fit 32 bits (checked at launch), so each load is a uniform 64-bit
+  // base plus one of these fixed 32-bit lane offsets.
+  const uint32_t row_bytes = row_elems * 2u;
+  uint32_t loff[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) loff[j] = (uint32_t)(4 * j + r) * row_bytes + 16u * c;
+
   // Issue the K and V loads of this wave's tile k. Tokens at or past seg_end
   // read the tile's first token instead (always valid), so no load touches an
   // unallocated block or a tail slot; their scores are masked in consume().
   auto issue = [&](int k, TileRegs& t) {
     const int ts = tile_start(k);
     if constexpr (kBlockUniform) {
-      // The 16 tokens of the tile share one block: scalar block-id load, a
-      // uniform 64-bit block base and 32-bit per-lane offsets inside it.
+      // The 16 tokens of the tile share one block: scalar block-id load and a
+      // uniform base at the tile's first slot.
       const uint32_t lb = fastdiv((uint32_t)ts, a.bs_div);
-      const int slot0 = ts - (int)lb * bs;
-      const size_t blk = (size_t)btc[lb] * ((size_t)bs * row_elems) + (size_t)hkv * kHeadDim;
-      const uint16_t* kblk = a.k_cache + blk;
-      const uint16_t* vblk = a.v_cache + blk;
+      const uint32_t slot0 = (uint32_t)ts - lb * (uint32_t)bs;
+      const size_t base = ((size_t)btc[lb] * bs + slot0) * row_bytes + (size_t)hkv * (kHeadDim * 2);
+      const auto kr = kv_rsrc(reinterpret_cast<const char*>(a.k_cache) + base);
+      const auto vr = kv_rsrc(reinterpret_cast<const char*>(a.v_cache) + base);
+      // No branch between full and partial tiles here: a uniform branch around
+      // the loads made the waits after it conservative (measured: 15% slower).
 #pragma unroll
       for (int j = 0; j < kLoads; ++j) {
-        const int tok = ts + 4 * j + r;
-        const uint32_t slot = tok < seg_end ? slot0 + 4 * j + r : slot0;
-        const uint32_t off = slot * row_elems + 8 * c;
-        t.k[j] = load_kv(kblk + off);
-        t.v[j] = load_kv(vblk + off);
+        const uint32_t off = ts + 4 * j + r < seg_end ? loff[j] : 16u * c;
+        t.k[j] = load_kv(kr, off);
+        t.v[j] = load_kv(vr, off);
       }
     } else {
 #pragma unroll
@@ -132,12 +143,15 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
     }
   };
 
-  auto consume = [&](int k, const TileRegs& t) {
+  // Fold tile k into st. kMasked: the tile may reach past seg_end (only a
+  // wave's last tile can, and the steady-state loop never consumes that one);
+  // scores of tokens at or past seg_end become -inf.
+  auto consume = [&](int k, const TileRegs& t, auto masked) {
+    constexpr bool kMasked = decltype(masked)::value;
     const int ts = tile_start(k);
-    float s[kLoads][GH];  // scores (base-2 units), then probabilities
+    float s[kLoads][GH];  // raw scores q.k, then probabilities
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
-      const bool valid = ts + 4 * j + r < seg_end;
 #pragma unroll
       for (int h = 0; h < GH; ++h) {
         float d = dot2_bf16(qf[h].x, t.k[j].x, 0.f);
@@ -145,21 +159,42 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
         d = dot2_bf16(qf[h].z, t.k[j].z, d);
         d = dot2_bf16(qf[h].w, t.k[j].w, d);
         d = row16_sum(d);
-        s[j][h] = valid ? d * a.scale_log2e : kNegInf;
+        if constexpr (kMasked) d = ts + 4 * j + r < seg_end ? d : kNegInf;
+        s[j][h] = d;
+      }
+    }
+    // New running max of each head in scaled base-2 units. The state is
+    // rescaled only when some head's max moved in some lane of the wave (a
+    // wave-uniform branch; after a segment's first tiles it is rare), and the
+    // factor of an unmoved head is exactly 1, so skipping changes no bit.
+    float mn[GH];
+    bool moved = false;
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
+      mn[h] = fmaxf(st.m[h], mt * a.scale_log2e);
+      moved |= mn[h] != st.m[h];
+    }
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+      for (int h = 0; h < GH; ++h) {
+        // m = -inf (no valid token yet) gives a factor of 0 on l = acc = 0.
+        const float al = mn[h] == st.m[h] ? 1.f : exp2_fast(st.m[h] - mn[h]);
+        st.m[h] = mn[h];
+        st.l[h] *= al;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) st.acc[h][d] *= al;
       }
     }
 #pragma unroll
     for (int h = 0; h < GH; ++h) {
-      const float mt = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
-      const float mn = fmaxf(st.m[h], mt);
-      const float ms = mn == kNegInf ? 0.f : mn;  // a row with no valid token yet
-      const float al = exp2_fast(st.m[h] - ms);
-      st.m[h] = mn;
+      // p = 2^(s * scale * log2(e) - m). Unmasked tiles make m finite; a row
+      // of a masked tile may have no valid token yet (m = -inf, scores -inf),
+      // and exp2(-inf) = 0 then needs a finite offset.
+      const float nm = kMasked && st.m[h] == kNegInf ? 0.f : -st.m[h];
 #pragma unroll
-      for (int j = 0; j < kLoads; ++j) s[j][h] = exp2_fast(s[j][h] - ms);
-      st.l[h] = fmaf(st.l[h], al, (s[0][h] + s[1][h]) + (s[2][h] + s[3][h]));
-#pragma unroll
-      for (int d = 0; d < 8; ++d) st.acc[h][d] *= al;
+      for (int j = 0; j < kLoads; ++j) s[j][h] = exp2_fast(fmaf(s[j][h], a.scale_log2e, nm));
+      st.l[h] += (s[0][h] + s[1][h]) + (s[2][h] + s[3][h]);
     }
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
@@ -172,6 +207,8 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
         for (int d = 0; d < 8; ++d) st.acc[h][d] = fmaf(s[j][h], vf[d], st.acc[h][d]);
     }
   };
+  constexpr std::true_type kTail{};
+  constexpr std::false_type kFull{};
 
   if (my_tiles > 0) {
     TileRegs t[DEPTH];
@@ -184,7 +221,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
       for (int i = 0; i < DEPTH; ++i) {
         issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
         if constexpr (kPinIssue) __builtin_amdgcn_sched_barrier(0);
-        consume(k + i, t[i]);
+        consume(k + i, t[i], kFull);
       }
     }
 #pragma unroll
@@ -192,7 +229,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
       if (k + i < my_tiles) {
         if (k + i + DEPTH - 1 < my_tiles) issue(k + i + DEPTH - 1, t[(i + DEPTH - 1) % DEPTH]);
         if constexpr (kPinIssue) __builtin_amdgcn_sched_barrier(0);
-        consume(k + i, t[i]);
+        consume(k + i, t[i], kTail);
       }
     }
 #pragma unroll
@@ -202,7 +239,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
       if (k + DEPTH + i < my_tiles) {
         if (k + DEPTH + i + DEPTH - 1 < my_tiles)
           issue(k + DEPTH + i + DEPTH - 1, t[(i + 2 * DEPTH - 1) % DEPTH]);
-        consume(k + DEPTH + i, t[(DEPTH + i) % DEPTH]);
+        consume(k + DEPTH + i, t[(DEPTH + i) % DEPTH], kTail);
       }
     }
   }
