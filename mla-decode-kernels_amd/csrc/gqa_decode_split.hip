@@ -292,7 +292,14 @@ extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
   return (size_t)B * Hq * num_splits * (gqa::kHeadDim + 2) * sizeof(float);
 }
 
-// Number of splits. Two bounds, the larger wins:
+// Number of splits. For the matrix-core scan's slot-group layout (groups of
+// 5-16 q-heads, 4 or 8 kv-heads; gqa_decode_mfma.hip): as many splits as give
+// every CU one workgroup (8 waves), rounded down, and no split longer than
+// kSlotChunk tokens. Measured on MI355X, 64Q/8KV: uniform B=32 S=32768 is
+// fastest at 8 splits (637 us; 666 at 16), uniform B=64 S=8192 at 4 (329 us);
+// ragged batches want more splits than the host can tell (B=32: 504 us at 8,
+// 447 at 32; B=128 with 16-token blocks: 1580 at 8, 1538 at 16).
+// Otherwise two bounds, the larger wins:
 //  * fill: as many waves as fit in one round of the target residency -- one
 //    wave per SIMD (4 per CU), or two for the matrix-core scan on long
 //    sequences, whose per-tile dependency chain needs a second wave per SIMD
@@ -319,6 +326,17 @@ extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size
   const int GH = mfma ? 16 : gqa::heads_per_wave(G);  // q-heads per wave
   const int P = gqa::kWavesPerHead;
   const int64_t s_max = (int64_t)max_blocks * block_size;
+  if (mfma && gqa::mfma_slot_shape(Hkv, G)) {
+    constexpr int64_t kSlotChunk = 4096;
+    int64_t ns = (int64_t)8 * num_cus / ((int64_t)B * Hkv);
+    const int64_t ns_len = (s_max + kSlotChunk - 1) / kSlotChunk;
+    if (ns < ns_len) ns = ns_len;
+    const int64_t ns_cap = s_max / 64 > 1 ? s_max / 64 : 1;  // splits of >= 64 tokens
+    if (ns > ns_cap) ns = ns_cap;
+    if (ns > kMaxSplits) ns = kMaxSplits;
+    if (ns < 1) ns = 1;
+    if (gqa::use_mfma_slot(B, Hkv, G, (int)ns, num_cus)) return (int)ns;
+  }
   const int waves_per_cu = (mfma && s_max >= kLongSequence) ? 8 : 4;
   const int64_t waves1 = (int64_t)B * Hkv * ((G + GH - 1) / GH) * P;
   const int64_t target = (int64_t)num_cus * waves_per_cu;

@@ -24,8 +24,21 @@ struct ScanArgs {
   float scale_log2e;  // scale * log2(e): scores are kept in base-2 units
 };
 
+// The matrix-core scan's slot-group layout (one workgroup of Hkv waves per
+// (split, request), one wave per kv-head) serves groups of at most 16 q-heads
+// with 4 or 8 kv-heads (16 would make 16-wave workgroups, whose register
+// budget spills) when the grid gives at least 3/4 of the CUs their full
+// residency of 8 waves (two per SIMD, which hides the scan's per-tile
+// dependency chain).
+inline bool mfma_slot_shape(int Hkv, int G) { return G <= 16 && (Hkv == 4 || Hkv == 8); }
+inline bool use_mfma_slot(int B, int Hkv, int G, int num_splits, int num_cus) {
+  return mfma_slot_shape(Hkv, G) && num_cus > 0 &&
+         (int64_t)B * num_splits * Hkv * 4 >= (int64_t)24 * num_cus;
+}
+
 // MFMA scan: QK^T and PV on v_mfma_f32_16x16x32_bf16, up to 16 q-heads of a
-// GQA group per wave. Launches one kernel over grid
+// GQA group per wave. Launches one kernel: the slot-group layout over grid
+// (num_splits, B) where use_mfma_slot says so, else over grid
 // (Hkv * ceil(G/16), B, num_splits); returns the launch status.
 hipError_t launch_scan_mfma(const ScanArgs& a, int B, hipStream_t stream);
 

@@ -56,6 +56,8 @@ WAVES_PER_HEAD = 4     # waves sharing a kv-head
 MIN_SPLIT_TOKENS = 2 * 16 * WAVES_PER_HEAD  # two 16-token tiles per wave
 MAX_CHUNK = 8192
 MAX_SPLITS = 32
+SLOT_CHUNK = 4096      # longest split of the matrix-core slot-group layout
+SLOT_WAVES_PER_CU = 8  # its residency: one workgroup of Hkv waves, two per SIMD
 
 
 def waves_per_split(B, Hq, Hkv):
@@ -69,14 +71,34 @@ def target_waves(Hq, Hkv, s_max, cus):
     return cus * (8 if mfma and s_max >= 8192 else 4)
 
 
-@pytest.mark.parametrize("Hq", [32, 64])
+def slot_shape(Hq, Hkv):
+    """Groups the matrix-core scan's slot-group layout serves."""
+    return 5 <= Hq // Hkv <= 16 and Hkv in (4, 8)
+
+
+def slot_eligible(B, Hkv, ns, cus):
+    """Its grid gives at least 3/4 of the CUs their 8 resident waves."""
+    return B * ns * Hkv * 4 >= 3 * SLOT_WAVES_PER_CU * cus
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (64, 8), (32, 4)])
 @pytest.mark.parametrize("B,max_blocks,bs", [(1, 1, 16), (1, 8, 16), (1, 32, 16), (1, 512, 64),
                                              (3, 512, 16), (8, 512, 64), (32, 512, 16),
+                                             (32, 512, 64), (64, 512, 16), (100, 512, 16),
                                              (128, 2048, 16), (4096, 64, 16), (2, 100000, 16)])
-def test_pick_num_splits_properties(B, max_blocks, bs, Hq):
-    cus, Hkv = 256, 8
+def test_pick_num_splits_properties(B, max_blocks, bs, Hq, Hkv):
+    cus = 256
     s_max = max_blocks * bs
     ns = capi.pick_num_splits(B, Hq, Hkv, bs, max_blocks, cus)
+    if slot_shape(Hq, Hkv):
+        # Slot-group layout: one workgroup per CU (rounded down), no split
+        # longer than SLOT_CHUNK, splits of at least 64 tokens, at most 32.
+        cap = min(MAX_SPLITS, max(1, s_max // 64))
+        fill = SLOT_WAVES_PER_CU * cus // (B * Hkv)
+        want = min(cap, max(fill, -(-s_max // SLOT_CHUNK), 1))
+        if slot_eligible(B, Hkv, want, cus):
+            assert ns == want
+            return
     per = waves_per_split(B, Hq, Hkv)
     target = target_waves(Hq, Hkv, s_max, cus)
     cap = min(MAX_SPLITS, max(1, s_max // MIN_SPLIT_TOKENS))
@@ -99,7 +121,7 @@ def test_pick_num_splits_headline_shapes():
     assert capi.pick_num_splits(1, 32, 8, 16, 32, 256) == 4
     assert capi.pick_num_splits(32, 32, 8, 16, 512, 256) == 1
     assert capi.pick_num_splits(8, 32, 8, 64, 512, 256) == 4
-    assert capi.pick_num_splits(32, 64, 8, 64, 512, 256) == 4
+    assert capi.pick_num_splits(32, 64, 8, 64, 512, 256) == 8  # slot-group layout
     assert capi.pick_num_splits(128, 32, 8, 16, 2048, 256) == 4
     prev = 0
     for B in (128, 32, 8, 1):
