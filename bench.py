@@ -14,8 +14,8 @@ torch.cuda.synchronize(). A v2 step is the C ABI's partial launch followed by
 its merge launch (one launch when num_splits is 1) on the current stream, with
 a caller-owned workspace. With --num-splits 0 (the default) the step is what
 the torch op's automatic choice runs: the token-balanced scan and its merge
-where gqa_decode_prefer_balanced says so (configs 3 and 5), else the split
-heuristic's count. HIP events are recorded only between groups of steps
+where gqa_decode_prefer_balanced says so (config 5), else the split
+heuristic's count (1 for config 2, 4 for config 3, 8 for config 4). HIP events are recorded only between groups of steps
 (an event between two kernels delays the second):
   value (median us)        median over the groups of the per-step average
   ms_per_step              host wall time of the K steps / K

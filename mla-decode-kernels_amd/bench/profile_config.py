@@ -88,7 +88,9 @@ def run_passes(config, out_dir, passes, timeout):
 # ------------------------------------------------------------------ summary
 
 def short_name(name):
-    """Kernel name without its argument list and 'void ' prefix."""
+    """Kernel name without its argument list, 'void ' prefix and anonymous
+    namespace qualifier."""
+    name = name.replace("(anonymous namespace)::", "")
     return re.sub(r"\(.*", "", name).replace("void ", "").strip()
 
 

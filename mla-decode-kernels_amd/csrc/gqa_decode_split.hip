@@ -294,11 +294,15 @@ extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
 
 // Number of splits. For the matrix-core scan's slot-group layout (groups of
 // 5-16 q-heads, 4 or 8 kv-heads; gqa_decode_mfma.hip): as many splits as give
-// every CU one workgroup (8 waves), rounded down, and no split longer than
-// kSlotChunk tokens. Measured on MI355X, 64Q/8KV: uniform B=32 S=32768 is
-// fastest at 8 splits (637 us; 666 at 16), uniform B=64 S=8192 at 4 (329 us);
-// ragged batches want more splits than the host can tell (B=32: 504 us at 8,
-// 447 at 32; B=128 with 16-token blocks: 1580 at 8, 1538 at 16).
+// every CU one workgroup (8 waves), rounded down, no split longer than
+// kSlotChunk tokens and none shorter than kSlotMinChunk -- when that grid does
+// not give the layout its residency, the head-strided rule below applies.
+// Measured on MI355X, 64Q/8KV: uniform B=32 S=32768 is fastest at 8 splits
+// (637 us; 666 at 16), uniform B=64 S=8192 at 4 (329 us); ragged batches want
+// more splits than the host can tell (B=32: 504 us at 8, 447 at 32; B=128
+// with 16-token blocks: 1580 at 8, 1538 at 16). Splits of 1024 tokens still
+// win (B=32 S=8192: 180 us at 8 vs 198 head-strided), splits of 256 lose
+// (B=32 S=2048: 56 us at 8 vs 50 for one head-strided pass).
 // Otherwise two bounds, the larger wins:
 //  * fill: as many waves as fit in one round of the target residency -- one
 //    wave per SIMD (4 per CU), or two for the matrix-core scan on long
@@ -328,10 +332,11 @@ extern "C" int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size
   const int64_t s_max = (int64_t)max_blocks * block_size;
   if (mfma && gqa::mfma_slot_shape(Hkv, G)) {
     constexpr int64_t kSlotChunk = 4096;
+    constexpr int64_t kSlotMinChunk = 1024;
     int64_t ns = (int64_t)8 * num_cus / ((int64_t)B * Hkv);
     const int64_t ns_len = (s_max + kSlotChunk - 1) / kSlotChunk;
     if (ns < ns_len) ns = ns_len;
-    const int64_t ns_cap = s_max / 64 > 1 ? s_max / 64 : 1;  // splits of >= 64 tokens
+    const int64_t ns_cap = s_max / kSlotMinChunk > 1 ? s_max / kSlotMinChunk : 1;
     if (ns > ns_cap) ns = ns_cap;
     if (ns > kMaxSplits) ns = kMaxSplits;
     if (ns < 1) ns = 1;

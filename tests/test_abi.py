@@ -57,6 +57,7 @@ MIN_SPLIT_TOKENS = 2 * 16 * WAVES_PER_HEAD  # two 16-token tiles per wave
 MAX_CHUNK = 8192
 MAX_SPLITS = 32
 SLOT_CHUNK = 4096      # longest split of the matrix-core slot-group layout
+SLOT_MIN_CHUNK = 1024  # its shortest
 SLOT_WAVES_PER_CU = 8  # its residency: one workgroup of Hkv waves, two per SIMD
 
 
@@ -92,8 +93,8 @@ def test_pick_num_splits_properties(B, max_blocks, bs, Hq, Hkv):
     ns = capi.pick_num_splits(B, Hq, Hkv, bs, max_blocks, cus)
     if slot_shape(Hq, Hkv):
         # Slot-group layout: one workgroup per CU (rounded down), no split
-        # longer than SLOT_CHUNK, splits of at least 64 tokens, at most 32.
-        cap = min(MAX_SPLITS, max(1, s_max // 64))
+        # longer than SLOT_CHUNK, none shorter than SLOT_MIN_CHUNK, at most 32.
+        cap = min(MAX_SPLITS, max(1, s_max // SLOT_MIN_CHUNK))
         fill = SLOT_WAVES_PER_CU * cus // (B * Hkv)
         want = min(cap, max(fill, -(-s_max // SLOT_CHUNK), 1))
         if slot_eligible(B, Hkv, want, cus):

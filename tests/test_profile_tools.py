@@ -72,3 +72,10 @@ def test_summarize(tmp_path):
     # 2^30 bytes per 524288 units = 2048 B per FETCH unit, 1024 per WRITE unit.
     assert traffic == (1001 * 2048, 8 * 1024)
     assert pc.traffic_line(root, "c5", traffic) == f"c5 v2 balanced {1001 * 2048} {8 * 1024}"
+
+
+def test_short_name_drops_signature_and_anonymous_namespace():
+    assert pc.short_name("void gqa::(anonymous namespace)::gqa_decode_mfma_kernel<8, 16, true, "
+                         "true>(gqa::ScanArgs)") == "gqa::gqa_decode_mfma_kernel<8, 16, true, true>"
+    assert pc.short_name("gqa::gqa_decode_merge_kernel(float const*, int)") == \
+        "gqa::gqa_decode_merge_kernel"
