@@ -61,8 +61,11 @@ GQA_DECODE_API int gqa_decode_v0_launch(const uint16_t* q, const uint16_t* k_cac
                          hipStream_t stream);
 
 /* v1: single-pass scan, one workgroup per (b, kv-head) holding the whole
- * q-head group, 16-byte row loads, fp32 online-softmax state.
- * Replaces gqa_decode_v1_launch (include/gqa_decode.h:12-16). */
+ * q-head group, 16-byte row loads, fp32 online-softmax state. Groups of 5-16
+ * q-heads over 4 or 8 kv-heads run the matrix-core scan, one workgroup per
+ * request with a wave per kv-head, when the batch alone fills the device
+ * (B * Hkv * 4 >= 24 * CUs). Replaces gqa_decode_v1_launch
+ * (include/gqa_decode.h:12-16). */
 GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cache,
                          const uint16_t* v_cache, const int* block_table,
                          const int* seq_lens, uint16_t* out, int B, int Hq,
@@ -71,7 +74,10 @@ GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cac
 
 /* v2: split-KV. A partial kernel writes one unnormalised fp32 (m, l, acc) state
  * per (b, q-head, split) to the caller's workspace, then a log-sum-exp merge
- * kernel writes `out`. Workspace layout (the reference's, v2_splitkv.cu:10-12):
+ * kernel writes `out`. Which scan runs depends on the shape, num_splits and the
+ * device's CU count (the layout rule of gqa_decode_v1_launch with
+ * B * num_splits in place of B), so results are bitwise reproducible for the
+ * same inputs, split count and device. Workspace layout (the reference's, v2_splitkv.cu:10-12):
  *   ws_acc [B, Hq, num_splits, 128] fp32, ws_m / ws_l [B, Hq, num_splits] fp32
  * ws_m holds the segment's max of scale*<q,k> (natural-log units), ws_l the sum
  * of exp(score - ws_m), ws_acc the exp-weighted sum of V rows. An empty segment
@@ -109,11 +115,14 @@ GQA_DECODE_API int gqa_decode_v2_merge_launch(const float* ws_acc, const float* 
  * workspace inline at python/gqa_decode_ext.cpp:106-109). */
 GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits);
 
-/* Split count that fills the device: as many (b, kv-head, split) waves as
- * fit one round of one wave per SIMD (two for the matrix-core scan on
- * sequences of 8192+ tokens), no split longer than 8192 tokens, each wave
- * keeping at least two 16-token tiles, and at most 32 splits.
- * max_blocks*block_size is taken as the longest sequence. num_cus <= 0 means
+/* Split count that fills the device. Groups of 5-16 q-heads over 4 or 8
+ * kv-heads: one workgroup of Hkv waves per CU (B * Hkv * splits = 8 * CUs,
+ * rounded down), no split longer than 4096 tokens nor shorter than 1024, at
+ * most 32 splits -- when that grid fills at least 3/4 of the CUs. Otherwise:
+ * as many (b, kv-head, split) waves as fit one round of one wave per SIMD (two
+ * for the matrix-core scan on sequences of 8192+ tokens), no split longer than
+ * 8192 tokens, each wave keeping at least two 16-token tiles, and at most 32
+ * splits. max_blocks*block_size is taken as the longest sequence. num_cus <= 0 means
  * "query the current device". Returns a value in [1, 32], or 0 for invalid
  * arguments. No reference counterpart: the reference defaults to 8
  * (python/gqa_decode_ext.cpp:133) and picks the best value by sweep
