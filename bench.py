@@ -14,8 +14,8 @@ torch.cuda.synchronize(). A v2 step is the C ABI's partial launch followed by
 its merge launch (one launch when num_splits is 1) on the current stream, with
 a caller-owned workspace. With --num-splits 0 (the default) the step is what
 the torch op's automatic choice runs: the token-balanced scan and its merge
-where gqa_decode_prefer_balanced says so (config 5), else the split
-heuristic's count (1 for config 2, 4 for config 3, 8 for config 4). HIP events are recorded only between groups of steps
+where gqa_decode_prefer_balanced says so (configs 4 and 5), else the split
+heuristic's count (1 for config 2, 4 for config 3). HIP events are recorded only between groups of steps
 (an event between two kernels delays the second):
   value (median us)        median over the groups of the per-step average
   ms_per_step              host wall time of the K steps / K
@@ -90,13 +90,13 @@ def read_traffic(config, kernel, num_splits):
 
 
 def kernel_name(kernel, group, balanced=False):
-    """The dominant kernel of one step: v0's kernel, the token-balanced scan,
-    else the scan kernel the dispatcher picks for this GQA group size (matrix
-    cores from 5 q-heads)."""
+    """The dominant kernel of one step: v0's kernel, else the token-balanced or
+    split-rule scan the dispatcher picks for this GQA group size (matrix cores
+    from 5 q-heads)."""
     if kernel == "v0":
         return "gqa_decode_v0_kernel"
     if balanced:
-        return "gqa_decode_balanced_kernel"
+        return "gqa_decode_balanced_mfma_kernel" if group >= 5 else "gqa_decode_balanced_kernel"
     return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
 
 

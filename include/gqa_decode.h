@@ -130,19 +130,23 @@ GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_split
 GQA_DECODE_API int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size,
                                int max_blocks, int num_cus);
 
-/* Largest GQA group (Hq / Hkv) the token-balanced launcher serves. */
-#define GQA_DECODE_BALANCED_MAX_GROUP 4
+/* Largest GQA group (Hq / Hkv) the token-balanced launcher serves: groups of
+ * up to 4 q-heads on the VALU scan (any Hkv), groups of 5-16 on the
+ * matrix-core scan with 4 or 8 kv-heads. */
+#define GQA_DECODE_BALANCED_MAX_GROUP 16
 /* Largest batch the token-balanced launcher serves. */
 #define GQA_DECODE_BALANCED_MAX_BATCH 20479
 
 /* Token-balanced split-KV: a persistent grid of num_workgroups workgroups
  * (<= 0: one per CU of the current device), each taking an equal share of the
- * batch's 16-token tiles in (request, kv-head) order, whatever the lengths;
- * segments cut at a share boundary are merged by a second kernel in share
- * order, so results are bitwise reproducible for a given num_workgroups (and
- * agree with v1/v2 within rounding, not bitwise). The host never reads
- * seq_lens. Lengths are clamped to max_blocks * block_size; a request of
- * length 0 gets NaN. Requires Hq / Hkv <= GQA_DECODE_BALANCED_MAX_GROUP and
+ * batch's 16-token tiles, whatever the lengths -- in (request, kv-head) order
+ * for groups of up to 4 q-heads, in request order (one wave per kv-head) for
+ * groups of 5-16; segments cut at a share boundary are merged by a second
+ * kernel in share order, so results are bitwise reproducible for a given
+ * num_workgroups (and agree with v1/v2 within rounding, not bitwise). The host
+ * never reads seq_lens. Lengths are clamped to max_blocks * block_size; a
+ * request of length 0 gets NaN. Requires Hq / Hkv <=
+ * GQA_DECODE_BALANCED_MAX_GROUP (with Hkv 4 or 8 for groups of 5+) and
  * B <= GQA_DECODE_BALANCED_MAX_BATCH (else hipErrorInvalidValue), and a
  * workspace of at least gqa_decode_balanced_workspace_bytes() bytes, 16-byte
  * aligned, whose contents need no initialisation. No reference counterpart:
@@ -181,13 +185,14 @@ GQA_DECODE_API int gqa_decode_balanced_merge_launch(
 /* 1 if gqa_decode_balanced_launch is expected to beat the split-KV launch with
  * gqa_decode_pick_num_splits' count for this shape on num_cus CUs (<= 0: the
  * current device), else 0 (also for shapes the balanced launcher does not
- * serve). The rule, from measurements on MI355X: groups of at most 4 q-heads,
- * a longest sequence (max_blocks * block_size) of at least 6144 tokens, at
- * least 32 MiB of KV (B * max_blocks * block_size tokens), at most 16
- * (request, kv-head) segments per CU, and not a split grid of exactly one
- * wave per SIMD with at most 8 splits (which uniform lengths make perfectly
- * even). This is the choice the torch op makes for num_splits=0. Pure host
- * code. No reference counterpart. */
+ * serve). The rule, from measurements on MI355X, with KV bytes counted at the
+ * longest sequence (max_blocks * block_size) for every request. Groups of at
+ * most 4 q-heads: a longest sequence of at least 6144 tokens, at least 32 MiB
+ * of KV, at most 16 (request, kv-head) segments per CU, and not a split grid
+ * of exactly one wave per SIMD with at most 8 splits (which uniform lengths
+ * make perfectly even). Groups of 5-16 q-heads over 4 or 8 kv-heads: at least
+ * 8 requests and 512 MiB of KV. This is the choice the torch op makes for
+ * num_splits=0. Pure host code. No reference counterpart. */
 GQA_DECODE_API int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size,
                                               int max_blocks, int num_cus);
 

@@ -12,7 +12,7 @@ pool of 1.1x the needed blocks):
   reference) of the baseline's run() only, v1, v2 at num_splits
   {1,4,8,16,32,64} (best recorded), v2's automatic choice (num_splits=0: the
   token-balanced launch or the split heuristic's count, recorded), the
-  token-balanced launch itself (groups of at most 4 q-heads), and v0 where it
+  token-balanced launch itself (every headtype of the grid), and v0 where it
   is not prohibitively slow (S <= 2048 and B <= 8);
 * 0.5 s of untimed calls (steady clocks), then each variant timed as the
   reference times it -- 10 warmup calls, 50 timed (30 for S=32768, B>=32),
@@ -107,7 +107,7 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
               else num_splits_heuristic(B, Hq, Hkv, bs, mb, num_cus))
     checks["v2_auto"] = cases.spot_check(
         lambda *a: gqa_decode_v2(*a, num_splits=0), case, scale, label="v2 automatic")
-    with_balanced = Hq // Hkv <= 4
+    with_balanced = Hq // Hkv <= 16  # the balanced launcher's groups (Hkv = 8 here)
     if with_balanced:
         checks["balanced"] = cases.spot_check(gqa_decode_balanced, case, scale, label="balanced")
 

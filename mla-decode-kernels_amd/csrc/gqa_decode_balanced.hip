@@ -26,6 +26,7 @@
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
 #include "gqa_scan.hpp"
+#include "gqa_scan_mfma.hpp"
 #include "gqa_scan_valu.hpp"
 #include "gqa_decode.h"
 
@@ -324,6 +325,177 @@ hipError_t launch_balanced_merge(const ScanArgs& a, const BalancedArgs& ba, hipS
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// The same token-balanced split-KV for groups of 5-16 q-heads, on the
+// matrix-core scan in its slot-group layout: a workgroup holds one wave per
+// kv-head (Hkv = 4 or 8), a segment is a whole request (T = sum_b
+// ceil(S_b / 16) tiles), and every wave scans each piece of its share for its
+// own kv-head, so the waves of a CU read each cache slot whole at about the
+// same time (see gqa_decode_mfma.hip). A piece that is a whole request is
+// normalised and written to `out`; a workgroup's first and last pieces go to
+// its two state slots, each holding all Hq q-heads.
+template <int NW, bool kBlockUniform>
+__global__ __launch_bounds__(64 * NW) void gqa_decode_balanced_mfma_kernel(const ScanArgs a,
+                                                                           const BalancedArgs ba) {
+  static_assert(kMTile == kTile, "the tile prefix sums count 16-token tiles");
+  __shared__ uint32_t pre[kBalancedTable];
+  __shared__ uint32_t wave_tot[NW];
+  __shared__ __attribute__((aligned(16))) uint8_t vlds_all[NW][kMTile * 256];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's kv-head
+  const int j = lane & 15, g = lane >> 4;
+  const int w = blockIdx.x;
+  const int B = ba.B, G = a.G, Hq = a.Hq;
+
+  tile_prefix<64 * NW>(a.seq_lens, B, ba.s_cap, pre, wave_tot);
+  const int T = (int)uniform(pre[B]);
+  const int t0 = share_start(w, T, ba.nwg), t1 = share_start(w + 1, T, ba.nwg);
+
+  // Requests without tokens sit at position pre[b] of the tile order; the
+  // first workgroup whose share ends at or after it writes their NaN.
+  for (int b = threadIdx.x; b < B; b += 64 * NW) {
+    const int p = (int)pre[b];
+    if (pre[b + 1] == pre[b] && t1 >= p && (w == 0 || t0 < p)) {
+      uint32_t* o = reinterpret_cast<uint32_t*>(a.out + (size_t)b * Hq * kHeadDim);
+      for (int i = 0; i < Hq * kHeadDim / 2; ++i) o[i] = 0x7fc07fc0u;  // bf16 quiet NaN pairs
+    }
+  }
+  if (t0 >= t1) {
+    if (threadIdx.x == 0) ba.meta[w] = ShareMeta{T, 0, 0, 0, 0, 0, 0, 0};
+    return;
+  }
+
+  int b = uniform(find_request(pre, B, 1, t0));
+  const int h0 = wv * G;  // the wave's q-heads: h0 .. h0 + G - 1
+  int t = t0;
+  for (int piece = 0; t < t1; ++piece) {
+    const int seg0 = (int)uniform(pre[b]);
+    const int n = (int)uniform(pre[b + 1]) - seg0;
+    const int lt0 = t - seg0;
+    const int lt1 = min(t1, seg0 + n) - seg0;
+    const int S = clamped_len(a, b, ba.s_cap);
+
+    uint4 qf[4];
+    mfma_load_q(a, b, h0, G, j, g, qf);
+    MfmaState st;
+    mfma_init(st);
+    mfma_scan_segment<kMTile, kBlockUniform>(a, a.block_table + (size_t)b * a.max_blocks, wv, qf,
+                                             kMTile * lt0, min(S, kMTile * lt1), 0, 1,
+                                             vlds_all[wv], j, g, st);
+    float Me[4], Le[4];
+    mfma_finish(st, g, Me, Le);
+
+    const bool whole = lt0 == 0 && lt1 == n;
+    // Only a workgroup's first and last pieces can be partial: slot 0 / 1.
+    float* slot = ba.states + ((size_t)w * 2 + (piece == 0 ? 0 : 1)) * Hq * kStateStride;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int h = 4 * g + e;
+      if (h >= G) continue;
+      if (whole) {
+        uint16_t* o = a.out + ((size_t)b * Hq + h0 + h) * kHeadDim;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+          o[16 * nb + j] = (uint16_t)f32_to_bf16_bits(finalize(st.o[nb][e], Le[e]));
+      } else {
+        float* sh = slot + (h0 + h) * kStateStride;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) sh[16 * nb + j] = st.o[nb][e];
+        if (j == 0) {
+          sh[kHeadDim] = Me[e];  // base-2 units
+          sh[kHeadDim + 1] = Le[e];
+        }
+      }
+    }
+
+    // The share's record, at its last piece (as in the VALU kernel above).
+    if (threadIdx.x == 0 && seg0 + lt1 >= t1)
+      ba.meta[w] = ShareMeta{T, seg0, seg0 + n, b, 0, lt0 == 0 && lt1 < n, 0, 0};
+    t = seg0 + lt1;
+    do {
+      ++b;
+    } while (b < B && uniform(pre[b + 1]) == uniform(pre[b]));
+  }
+}
+
+// Workgroup (w, y) merges q-heads y * NWM .. y * NWM + NWM - 1 of the request
+// whose first cut is the boundary after share w (its record says so;
+// otherwise it exits at once). The request's pieces are in shares
+// w .. vend - 1, found as in the VALU merge. Each wave folds one head's pieces
+// in share order with an online merge (lane l owns dims 2l, 2l + 1), loading
+// kBatch pieces at a time: bitwise reproducible for a given number of
+// workgroups. One wave per head keeps the merge to one or two memory round
+// trips (a workgroup walking the heads in turn took ~30 us on config 4).
+template <int NWM>
+__global__ __launch_bounds__(64 * NWM) void gqa_decode_balanced_mfma_merge_kernel(
+    const ScanArgs a, const BalancedArgs ba) {
+  constexpr int kBatch = 8;  // pieces a wave loads together
+  const int w = blockIdx.x;
+  const ShareMeta meta = ba.meta[w];
+  if (!meta.merge) return;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * NWM + (threadIdx.x >> 6);
+  const int nwg = ba.nwg, Hq = a.Hq;
+  if (h >= Hq) return;
+  const int T = meta.T, seg0 = meta.seg0, seg1 = meta.seg1;
+  const int vend = (int)min((int64_t)nwg, ((int64_t)seg1 * nwg + T - 1) / T);
+  float M = kNegInf, L = 0.f;
+  float2 A = make_float2(0.f, 0.f);
+  for (int v = w; v < vend; v += kBatch) {
+    float mv[kBatch], lv[kBatch];
+    float2 av[kBatch];
+    bool live[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int u = v + k;
+      const int u0 = share_start(u, T, nwg), u1 = share_start(u + 1, T, nwg);
+      live[k] = u < vend && u1 > u0;  // an empty share holds no piece
+      const float* sh = ba.states +
+                        ((size_t)(live[k] ? u : w) * 2 + (u0 < seg0 ? 1 : 0)) * Hq * kStateStride +
+                        (size_t)h * kStateStride;
+      mv[k] = sh[kHeadDim];
+      lv[k] = sh[kHeadDim + 1];
+      av[k] = reinterpret_cast<const float2*>(sh)[lane];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (!live[k]) continue;
+      const float mn = fmaxf(M, mv[k]);
+      const float ms = mn == kNegInf ? 0.f : mn;
+      const float fa = exp2_fast(M - ms), fv = exp2_fast(mv[k] - ms);
+      L = fmaf(L, fa, lv[k] * fv);
+      A.x = fmaf(A.x, fa, av[k].x * fv);
+      A.y = fmaf(A.y, fa, av[k].y * fv);
+      M = mn;
+    }
+  }
+  const uint32_t lo = f32_to_bf16_bits(finalize(A.x, L));
+  const uint32_t hi = f32_to_bf16_bits(finalize(A.y, L));
+  reinterpret_cast<uint32_t*>(a.out + ((size_t)meta.b * Hq + h) * kHeadDim)[lane] =
+      lo | (hi << 16);
+}
+
+template <int NW>
+hipError_t launch_balanced_mfma_partial(const ScanArgs& a, const BalancedArgs& ba,
+                                        hipStream_t stream) {
+  if (a.block_size % kMTile == 0)
+    hipLaunchKernelGGL((gqa_decode_balanced_mfma_kernel<NW, true>), dim3(ba.nwg), dim3(64 * NW),
+                       0, stream, a, ba);
+  else
+    hipLaunchKernelGGL((gqa_decode_balanced_mfma_kernel<NW, false>), dim3(ba.nwg), dim3(64 * NW),
+                       0, stream, a, ba);
+  return hipGetLastError();
+}
+
+hipError_t launch_balanced_mfma_merge(const ScanArgs& a, const BalancedArgs& ba,
+                                      hipStream_t stream) {
+  if (ba.nwg < 2) return hipSuccess;  // one share: every piece was whole
+  hipLaunchKernelGGL((gqa_decode_balanced_mfma_merge_kernel<4>),
+                     dim3(ba.nwg - 1, (a.Hq + 3) / 4), dim3(256), 0, stream, a, ba);
+  return hipGetLastError();
+}
+
 int balanced_workgroups(int num_workgroups) {
   return num_workgroups > 0 ? num_workgroups : device_cu_count();
 }
@@ -334,10 +506,12 @@ extern "C" size_t gqa_decode_balanced_workspace_bytes(int B, int Hq, int Hkv, in
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0) return 0;
   const int G = Hq / Hkv;
   if (G > GQA_DECODE_BALANCED_MAX_GROUP) return 0;
+  if (gqa::use_mfma(G) && !gqa::mfma_slot_shape(Hkv, G)) return 0;
   const int nwg = gqa::balanced_workgroups(num_workgroups);
   if (nwg <= 0) return 0;
-  return gqa::balanced_states_bytes(nwg, gqa::heads_per_wave(G)) +
-         (size_t)nwg * sizeof(gqa::ShareMeta);
+  // State slots hold one kv-head's q-heads (VALU scan) or all Hq (MFMA scan).
+  const int slot_heads = gqa::use_mfma(G) ? Hq : gqa::heads_per_wave(G);
+  return gqa::balanced_states_bytes(nwg, slot_heads) + (size_t)nwg * sizeof(gqa::ShareMeta);
 }
 
 namespace {
@@ -356,9 +530,13 @@ int balanced_launch(BalancedPart part, const uint16_t* q, const uint16_t* k_cach
   if (B == 0) return hipSuccess;
   const int G = Hq / Hkv;
   if (G > GQA_DECODE_BALANCED_MAX_GROUP || B > gqa::kBalancedMaxB) return hipErrorInvalidValue;
+  const bool mfma = gqa::use_mfma(G);
+  if (mfma && !gqa::mfma_slot_shape(Hkv, G)) return hipErrorInvalidValue;
   const int64_t s_cap = (int64_t)max_blocks * block_size;
-  // Every tile index of the batch, Hkv * sum_b ceil(S_b / 16), fits in 31 bits.
-  if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31))
+  // Every tile index of the batch, segs * sum_b ceil(S_b / 16), fits in 31 bits
+  // (Hkv segments per request for the VALU scan, one for the MFMA scan).
+  const int64_t segs = mfma ? 1 : Hkv;
+  if (segs * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31))
     return hipErrorInvalidValue;
   const int nwg = gqa::balanced_workgroups(num_workgroups);
   if (nwg <= 0) return hipErrorInvalidValue;
@@ -381,11 +559,20 @@ int balanced_launch(BalancedPart part, const uint16_t* q, const uint16_t* k_cach
   a.num_splits = 1;
   a.bs_div = gqa::make_fastdiv((uint32_t)block_size);
   a.scale_log2e = (float)((double)scale * 1.4426950408889634);
-  const size_t states = gqa::balanced_states_bytes(nwg, gqa::heads_per_wave(G));
+  const size_t states =
+      gqa::balanced_states_bytes(nwg, mfma ? Hq : gqa::heads_per_wave(G));
   const gqa::BalancedArgs ba{workspace,
                              reinterpret_cast<gqa::ShareMeta*>(
                                  reinterpret_cast<char*>(workspace) + states),
                              B, nwg, (int)s_cap};
+  if (mfma) {
+    if (part != BalancedPart::kMerge) {
+      const hipError_t e = Hkv == 4 ? gqa::launch_balanced_mfma_partial<4>(a, ba, stream)
+                                    : gqa::launch_balanced_mfma_partial<8>(a, ba, stream);
+      if (e != hipSuccess || part == BalancedPart::kPartial) return e;
+    }
+    return gqa::launch_balanced_mfma_merge(a, ba, stream);
+  }
   auto run = [&](auto gh) -> int {
     constexpr int GH = decltype(gh)::value;
     if (part != BalancedPart::kMerge) {
@@ -444,21 +631,38 @@ extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size
   // pipeline at each piece stays cheap. It loses a few percent where the split
   // grid is exactly one round of one wave per SIMD with few splits (uniform
   // lengths make that perfect) and on short or small batches.
-  // Preferred when: groups of at most 4 q-heads, sequences up to at least
+  // Groups of at most 4 q-heads: preferred when sequences reach at least
   // kMinLongest tokens, at least kMinBytes of KV, at most kMaxSegmentsPerCu
   // segments per CU, and a split grid that is not exactly one round of at
   // most kMaxEvenSplits splits.
+  // Groups of 5-16 q-heads over 4 or 8 kv-heads (the matrix-core scan): the
+  // balanced launch is within 1.5 % of the best split count on uniform
+  // batches of at least kMfmaMinBatch requests and kMfmaMinBytes of KV
+  // (64Q/8KV: B=32 S=32768 640 vs 637 us; B=64 S=8192 333 vs 329; B=16 S=8192
+  // 95.0 vs 95.5) and far ahead on ragged ones (B=32: 344 vs 447; B=128: 1201
+  // vs 1536; B=8: 100 vs 140); with fewer requests each is cut into many
+  // pieces and the merge costs more (B=1 S=32768: 81 vs 36 us; B=8 S=8192: 59
+  // vs 51), so below either bound the split launch runs.
   constexpr int64_t kMinLongest = 6144;
   constexpr int64_t kMinBytes = int64_t(32) << 20;
   constexpr int kMaxSegmentsPerCu = 16;
   constexpr int kMaxEvenSplits = 8;
+  constexpr int kMfmaMinBatch = 8;
+  constexpr int64_t kMfmaMinBytes = int64_t(512) << 20;
   if (num_cus <= 0 && (num_cus = gqa::device_cu_count()) <= 0) return 0;
   if (B < 1 || Hkv < 1 || Hq % Hkv != 0 || Hq / Hkv > GQA_DECODE_BALANCED_MAX_GROUP ||
       B > gqa::kBalancedMaxB || block_size < 1 || max_blocks < 1)
     return 0;
+  const int G = Hq / Hkv;
   const int64_t s_cap = (int64_t)max_blocks * block_size;
+  const int64_t kv_bytes = (int64_t)B * s_cap * Hkv * gqa::kHeadDim * 4;
+  if (gqa::use_mfma(G)) {
+    if (!gqa::mfma_slot_shape(Hkv, G)) return 0;
+    if ((int64_t)B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31)) return 0;
+    return B >= kMfmaMinBatch && kv_bytes >= kMfmaMinBytes ? 1 : 0;
+  }
   if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31)) return 0;
-  if (s_cap < kMinLongest || (int64_t)B * s_cap * Hkv * gqa::kHeadDim * 4 < kMinBytes) return 0;
+  if (s_cap < kMinLongest || kv_bytes < kMinBytes) return 0;
   if ((int64_t)B * Hkv > (int64_t)kMaxSegmentsPerCu * num_cus) return 0;
   const int ns = gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus);
   const int64_t split_waves = (int64_t)B * Hkv * gqa::kWavesPerHead * ns;

@@ -28,14 +28,6 @@
 
 namespace gqa {
 
-// GQA groups larger than this run the matrix-core scan (gqa_decode_mfma.hip):
-// its VALU work per tile does not grow with the group, while this kernel's
-// does (measured: 8-head groups are VALU-bound here at ~60% of HBM peak and
-// reach ~72% on MFMA; 4-head groups stream ~5% faster here).
-#ifndef GQA_MFMA_MIN_GROUP
-#define GQA_MFMA_MIN_GROUP 5
-#endif
-
 // One workgroup = P waves on one kv-head of one request b, one q-head chunk of
 // GH heads and one split; wave w takes tiles w, w + P, ... of the segment.
 // Single-pass launches (num_splits == 1) with `out` set write the normalised
@@ -166,8 +158,6 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(const float* __re
   const uint32_t hi = f32_to_bf16_bits(finalize(A1, L));
   reinterpret_cast<uint32_t*>(out + (size_t)bh * kHeadDim)[lane] = lo | (hi << 16);
 }
-
-inline bool use_mfma(int G) { return G >= GQA_MFMA_MIN_GROUP; }
 
 template <int GH, int P>
 hipError_t launch_scan_shape(const ScanArgs& a, dim3 grid, hipStream_t stream) {

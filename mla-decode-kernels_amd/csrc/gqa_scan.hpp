@@ -24,6 +24,15 @@ struct ScanArgs {
   float scale_log2e;  // scale * log2(e): scores are kept in base-2 units
 };
 
+// GQA groups of at least this many q-heads run the matrix-core scan
+// (gqa_scan_mfma.hpp): its VALU work per tile does not grow with the group,
+// while the VALU scan's does (measured: 8-head groups are VALU-bound on the
+// VALU scan at ~60% of HBM peak; 4-head groups stream ~5% faster there).
+#ifndef GQA_MFMA_MIN_GROUP
+#define GQA_MFMA_MIN_GROUP 5
+#endif
+inline bool use_mfma(int G) { return G >= GQA_MFMA_MIN_GROUP; }
+
 // The matrix-core scan's slot-group layout (one workgroup of Hkv waves per
 // (split, request), one wave per kv-head) serves groups of at most 16 q-heads
 // with 4 or 8 kv-heads (16 would make 16-wave workgroups, whose register

@@ -134,7 +134,7 @@ torch::Tensor run_balanced(const GqaDims& d, const torch::Tensor& q, const torch
   const int nwg = num_workgroups > 0 ? (int)num_workgroups : device_cus(q);
   const size_t bytes = gqa_decode_balanced_workspace_bytes((int)d.B, (int)d.Hq, (int)d.Hkv, nwg);
   TORCH_CHECK(bytes > 0, "the balanced launch serves GQA groups of at most ",
-              GQA_DECODE_BALANCED_MAX_GROUP, " q-heads");
+              GQA_DECODE_BALANCED_MAX_GROUP, " q-heads (4 or 8 kv-heads for groups of 5+)");
   auto out = torch::empty_like(q);
   auto ws = torch::empty({(int64_t)((bytes + 3) / 4)},
                          torch::TensorOptions().dtype(torch::kFloat32).device(q.device()));

@@ -179,16 +179,21 @@ def test_v2_rejects_missing_workspace(which):
 
 
 @pytest.mark.parametrize("Hq,Hkv,nwg,gh", [(32, 8, 256, 4), (8, 8, 256, 1), (16, 8, 7, 2),
-                                          (24, 8, 256, 4), (4, 1, 1, 4)])
+                                          (24, 8, 256, 4), (4, 1, 1, 4),
+                                          # groups of 5-16 (matrix-core scan): all Hq heads
+                                          (64, 8, 256, 64), (40, 8, 3, 40), (128, 8, 256, 128),
+                                          (32, 4, 256, 32), (64, 4, 5, 64)])
 def test_balanced_workspace_bytes(Hq, Hkv, nwg, gh):
     # Two partial states (first and last piece) per workgroup, 132 floats per
-    # head, then a 32-byte share record per workgroup at a 16-byte boundary.
+    # head of a slot, then a 32-byte share record per workgroup at a 16-byte
+    # boundary. A slot holds one kv-head's q-heads (VALU scan) or all Hq.
     states = (nwg * 2 * gh * 132 * 4 + 15) // 16 * 16
     assert capi.balanced_workspace_bytes(32, Hq, Hkv, nwg) == states + nwg * 32
 
 
-@pytest.mark.parametrize("args", [(0, 32, 8, 256), (32, 64, 8, 256), (32, 30, 8, 256),
-                                  (32, 32, 0, 256)])
+@pytest.mark.parametrize("args", [(0, 32, 8, 256), (32, 136, 8, 256), (32, 30, 8, 256),
+                                  (32, 32, 0, 256), (32, 48, 6, 256), (32, 128, 16, 256),
+                                  (32, 16, 2, 256)])
 def test_balanced_workspace_bytes_invalid(args):
     assert capi.balanced_workspace_bytes(*args) == 0
 
@@ -203,9 +208,12 @@ def test_balanced_rejects_bad_arguments(over):
 
 
 def test_balanced_rejects_unsupported_shapes():
-    # Groups above 4 q-heads, batches beyond the LDS prefix table, workspace
-    # missing or too small for the workgroup count.
-    assert capi.balanced_launch(*balanced_args(Hq=64)) == INVALID
+    # Groups above 16 q-heads, groups of 5+ over other than 4 or 8 kv-heads,
+    # batches beyond the LDS prefix table, workspace missing or too small for
+    # the workgroup count.
+    assert capi.balanced_launch(*balanced_args(Hq=136)) == INVALID
+    assert capi.balanced_launch(*balanced_args(Hq=96, Hkv=12)) == INVALID
+    assert capi.balanced_launch(*balanced_args(Hq=64, Hkv=8, ws_bytes=1 << 20)) == INVALID
     assert capi.balanced_launch(*balanced_args(B=20480)) == INVALID
     args = balanced_args()
     args[-3] = None
@@ -215,33 +223,42 @@ def test_balanced_rejects_unsupported_shapes():
 
 
 @pytest.mark.parametrize("fn", ["balanced_partial_launch", "balanced_merge_launch"])
-@pytest.mark.parametrize("over", BAD + [dict(Hq=64), dict(B=20480)])
+@pytest.mark.parametrize("over", BAD + [dict(Hq=136), dict(Hq=96, Hkv=12), dict(B=20480)])
 def test_balanced_parts_reject_bad_arguments(fn, over):
     assert getattr(capi, fn)(*balanced_args(**over)) == INVALID
 
 
 def test_prefer_balanced_headline_shapes():
-    # BASELINE configs 1..5 on 256 CUs: balanced for the ragged config (5);
-    # the split path where the split grid is exactly one wave per SIMD (2, 3),
-    # for 8-head groups (4) and for tiny batches (1).
+    # BASELINE configs 1..5 on 256 CUs: balanced for the ragged config (5) and
+    # the 8-head groups (4, whose lengths the host cannot tell from ragged
+    # ones); the split path where the split grid is exactly one wave per SIMD
+    # (2, 3) and for tiny batches (1).
     shapes = [(1, 32, 16, 32), (32, 32, 16, 512), (8, 32, 64, 512), (32, 64, 64, 512),
               (128, 32, 16, 2048)]
     assert [capi.prefer_balanced(B, Hq, 8, bs, mb, 256) for B, Hq, bs, mb in shapes] == \
-        [0, 0, 0, 0, 1]
+        [0, 0, 0, 1, 1]
 
 
 @pytest.mark.parametrize("B,Hq,bs,mb", [(1, 32, 16, 2048), (8, 32, 16, 512), (32, 32, 64, 512),
                                         (128, 32, 16, 2048), (256, 32, 16, 2048), (1, 32, 16, 64),
                                         (4, 16, 16, 4096), (2, 64, 16, 4096), (128, 32, 16, 512),
                                         (64, 32, 16, 512), (600, 32, 16, 1024), (3, 24, 16, 2048),
-                                        (1, 32, 16, 512), (128, 32, 16, 511), (512, 32, 16, 256)])
+                                        (1, 32, 16, 512), (128, 32, 16, 511), (512, 32, 16, 256),
+                                        # groups of 5-16 (matrix-core scan)
+                                        (32, 64, 64, 512), (8, 64, 16, 2048), (8, 64, 16, 512),
+                                        (7, 64, 64, 2048), (16, 64, 16, 512), (16, 64, 16, 511),
+                                        (128, 64, 16, 128), (4, 128, 64, 512), (64, 40, 16, 512)])
 def test_prefer_balanced_rule(B, Hq, bs, mb):
     # The documented rule, clause by clause.
     Hkv, cus = 8, 256
     s_max = mb * bs
     ns = capi.pick_num_splits(B, Hq, Hkv, bs, mb, cus)
-    want = (Hq // Hkv <= 4 and s_max >= 6144 and B * s_max * Hkv * 512 >= 32 << 20
-            and B * Hkv <= 16 * cus and not (B * Hkv * 4 * ns == 4 * cus and ns <= 8))
+    kv_bytes = B * s_max * Hkv * 512
+    if Hq // Hkv >= 5:
+        want = Hq // Hkv <= 16 and B >= 8 and kv_bytes >= 512 << 20
+    else:
+        want = (s_max >= 6144 and kv_bytes >= 32 << 20 and B * Hkv <= 16 * cus
+                and not (B * Hkv * 4 * ns == 4 * cus and ns <= 8))
     assert capi.prefer_balanced(B, Hq, Hkv, bs, mb, cus) == int(want)
 
 
@@ -249,6 +266,9 @@ def test_prefer_balanced_invalid():
     assert capi.prefer_balanced(0, 32, 8, 16, 512, 256) == 0
     assert capi.prefer_balanced(8, 30, 8, 16, 512, 256) == 0
     assert capi.prefer_balanced(20480, 32, 8, 16, 16, 256) == 0
+    # Groups of 5+ over other than 4 or 8 kv-heads, and groups above 16.
+    assert capi.prefer_balanced(64, 96, 12, 16, 2048, 256) == 0
+    assert capi.prefer_balanced(64, 136, 8, 16, 2048, 256) == 0
 
 
 def test_empty_batch_is_a_no_op():

@@ -147,6 +147,6 @@ def test_balanced_ops(gpu):
     assert torch.equal(gqa_decode_balanced(*case, SCALE), want)
     assert torch.equal(gqa_decode_v2(*case, SCALE, num_splits=0), want)
     assert torch.equal(gqa_decode_balanced(*case, SCALE, num_workgroups=7), balanced(case, nwg=7))
-    with pytest.raises(RuntimeError, match="at most 4"):
-        gqa_decode_balanced(torch.zeros(1, 64, 128, dtype=torch.bfloat16, device=q.device), k, v,
+    with pytest.raises(RuntimeError, match="at most 16"):
+        gqa_decode_balanced(torch.zeros(1, 136, 128, dtype=torch.bfloat16, device=q.device), k, v,
                             bt[:1], sl[:1], SCALE)
