@@ -89,14 +89,16 @@ def read_traffic(config, kernel, num_splits):
     return None
 
 
-def kernel_name(kernel, group, balanced=False):
+def kernel_name(kernel, group, balanced=False, hkv=8):
     """The dominant kernel of one step: v0's kernel, else the token-balanced or
-    split-rule scan the dispatcher picks for this GQA group size (matrix cores
-    from 5 q-heads)."""
+    split-rule scan the dispatcher picks: split launches use the matrix cores
+    from 5 q-heads per group, the balanced launcher whenever there are 4 or 8
+    kv-heads."""
     if kernel == "v0":
         return "gqa_decode_v0_kernel"
     if balanced:
-        return "gqa_decode_balanced_mfma_kernel" if group >= 5 else "gqa_decode_balanced_kernel"
+        return ("gqa_decode_balanced_mfma_kernel" if hkv in (4, 8)
+                else "gqa_decode_balanced_kernel")
     return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
 
 
@@ -284,7 +286,7 @@ def main(argv=None):
         "kv_bytes": kvb,
         "sol_us": round(sol, 3),
         "op_median_us": round(op_ms * 1e3, 3),
-        "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv, balanced),
+        "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv, balanced, Hkv),
                      "achieved": round(achieved, 1),
                      "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
                      "avg_kernel_us": round(kern_avg_us, 3),

@@ -130,18 +130,19 @@ GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_split
 GQA_DECODE_API int gqa_decode_pick_num_splits(int B, int Hq, int Hkv, int block_size,
                                int max_blocks, int num_cus);
 
-/* Largest GQA group (Hq / Hkv) the token-balanced launcher serves: groups of
- * up to 4 q-heads on the VALU scan (any Hkv), groups of 5-16 on the
- * matrix-core scan with 4 or 8 kv-heads. */
+/* Largest GQA group (Hq / Hkv) the token-balanced launcher serves: up to 16
+ * q-heads with 4 or 8 kv-heads (matrix-core scan), up to 4 with other kv-head
+ * counts (VALU scan). */
 #define GQA_DECODE_BALANCED_MAX_GROUP 16
 /* Largest batch the token-balanced launcher serves. */
 #define GQA_DECODE_BALANCED_MAX_BATCH 20479
 
 /* Token-balanced split-KV: a persistent grid of num_workgroups workgroups
  * (<= 0: one per CU of the current device), each taking an equal share of the
- * batch's 16-token tiles, whatever the lengths -- in (request, kv-head) order
- * for groups of up to 4 q-heads, in request order (one wave per kv-head) for
- * groups of 5-16; segments cut at a share boundary are merged by a second
+ * batch's 16-token tiles, whatever the lengths -- in request order on the
+ * matrix-core scan (one wave per kv-head) for 4 or 8 kv-heads, in
+ * (request, kv-head) order on the VALU scan for other kv-head counts (groups
+ * of up to 4 q-heads); segments cut at a share boundary are merged by a second
  * kernel in share order, so results are bitwise reproducible for a given
  * num_workgroups (and agree with v1/v2 within rounding, not bitwise). The host
  * never reads seq_lens. Lengths are clamped to max_blocks * block_size; a

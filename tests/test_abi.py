@@ -179,14 +179,18 @@ def test_v2_rejects_missing_workspace(which):
 
 
 @pytest.mark.parametrize("Hq,Hkv,nwg,gh", [(32, 8, 256, 4), (8, 8, 256, 1), (16, 8, 7, 2),
-                                          (24, 8, 256, 4), (4, 1, 1, 4),
+                                          (24, 8, 256, 4), (4, 1, 1, 4), (64, 16, 256, 4),
+                                          (6, 2, 9, 4), (32, 16, 3, 2), (16, 16, 256, 1),
                                           # groups of 5-16 (matrix-core scan): all Hq heads
                                           (64, 8, 256, 64), (40, 8, 3, 40), (128, 8, 256, 128),
                                           (32, 4, 256, 32), (64, 4, 5, 64)])
 def test_balanced_workspace_bytes(Hq, Hkv, nwg, gh):
     # Two partial states (first and last piece) per workgroup, 132 floats per
     # head of a slot, then a 32-byte share record per workgroup at a 16-byte
-    # boundary. A slot holds one kv-head's q-heads (VALU scan) or all Hq.
+    # boundary. A slot holds all Hq q-heads with 4 or 8 kv-heads (matrix-core
+    # scan), else one kv-head's q-heads rounded to 1, 2 or 4 (VALU scan).
+    if Hkv in (4, 8):
+        gh = Hq
     states = (nwg * 2 * gh * 132 * 4 + 15) // 16 * 16
     assert capi.balanced_workspace_bytes(32, Hq, Hkv, nwg) == states + nwg * 32
 

@@ -1,5 +1,11 @@
 """GPU parity of the token-balanced split-KV launcher (gqa_decode_balanced_launch).
 
+With 4 or 8 kv-heads the launcher runs the matrix-core scan (one wave per
+kv-head; tests/test_balanced_mfma.py covers its groups of 5-16), with other
+kv-head counts the VALU scan over (request, kv-head) segments: the tests
+below run both, the reference's 8 kv-heads and the same groups over 16 (or 2
+and 1) kv-heads.
+
 Same inputs, poisoning and tolerance as the reference's kernel tests
 (tests/test_gqa_decode.py:27-139 of the reference: 0.5 * N(0,1), shuffled 2x
 pool, NaN in every slot that must not be read, atol = rtol = 2e-2), against
@@ -53,10 +59,14 @@ GRID = {k: v for k, v in CASES.items() if v["Hq"] // v["Hkv"] <= 4}
 
 
 @pytest.mark.parametrize("name", list(GRID))
-def test_balanced_reference_grid(gpu, name):
-    print(f"balanced {name}", flush=True)
-    case = ref_case(GRID[name])
-    assert_close(balanced(case), numpy_oracle(case, SCALE), ATOL, RTOL, f"balanced/{name}")
+@pytest.mark.parametrize("hkv", [8, 16])
+def test_balanced_reference_grid(gpu, name, hkv):
+    print(f"balanced {name} Hkv={hkv}", flush=True)
+    cfg = dict(GRID[name])
+    cfg["Hq"], cfg["Hkv"] = cfg["Hq"] // cfg["Hkv"] * hkv, hkv
+    case = ref_case(cfg)
+    assert_close(balanced(case), numpy_oracle(case, SCALE), ATOL, RTOL,
+                 f"balanced/{name}/Hkv{hkv}")
 
 
 @pytest.mark.parametrize("nwg", [1, 2, 3, 7, 64, 256, 1000])
@@ -65,25 +75,30 @@ def test_balanced_workgroup_counts(gpu, nwg):
     # the first case: most shares empty.
     print(f"balanced nwg={nwg}", flush=True)
     for cfg in (dict(S_list=[100, 257, 33, 1], Hq=32, Hkv=8, bs=16),
-                dict(S_list=[4000, 17, 900], Hq=16, Hkv=4, bs=16)):
+                dict(S_list=[4000, 17, 900], Hq=16, Hkv=4, bs=16),
+                dict(S_list=[100, 257, 33, 1], Hq=64, Hkv=16, bs=16),
+                dict(S_list=[4000, 17, 900], Hq=8, Hkv=2, bs=16)):
         case = ref_case(cfg, seed=nwg)
         assert_close(balanced(case, nwg=nwg), numpy_oracle(case, SCALE), ATOL, RTOL, f"nwg{nwg}")
 
 
 @pytest.mark.parametrize("G", [1, 2, 3, 4])
 @pytest.mark.parametrize("bs", [1, 7, 16, 24, 64])
-def test_balanced_groups_and_block_sizes(gpu, G, bs):
-    print(f"balanced G={G} bs={bs}", flush=True)
-    cfg = dict(S_list=[1, 50, 333, 129, 700], Hq=4 * G, Hkv=4, bs=bs)
-    case = ref_case(cfg, seed=G * 100 + bs)
-    assert_close(balanced(case, nwg=37), numpy_oracle(case, SCALE), ATOL, RTOL, f"G{G}/bs{bs}")
+@pytest.mark.parametrize("hkv", [4, 2, 1])
+def test_balanced_groups_and_block_sizes(gpu, G, bs, hkv):
+    print(f"balanced G={G} bs={bs} Hkv={hkv}", flush=True)
+    cfg = dict(S_list=[1, 50, 333, 129, 700], Hq=hkv * G, Hkv=hkv, bs=bs)
+    case = ref_case(cfg, seed=G * 100 + bs + hkv)
+    assert_close(balanced(case, nwg=37), numpy_oracle(case, SCALE), ATOL, RTOL,
+                 f"G{G}/bs{bs}/Hkv{hkv}")
 
 
-def test_balanced_zero_length_requests(gpu):
+@pytest.mark.parametrize("hkv", [8, 16])
+def test_balanced_zero_length_requests(gpu, hkv):
     # seq_len 0 is unsupported (NaN, as in the reference); the other requests
     # must be unaffected, whichever share the empty ones fall into.
     S_list = [0, 37, 0, 0, 100, 0]
-    case = make_case(S_list, 32, 8, 16, pool_factor=2, seed=5, qkv_std=0.5, poison=True)
+    case = make_case(S_list, 4 * hkv, hkv, 16, pool_factor=2, seed=5, qkv_std=0.5, poison=True)
     live = [i for i, s in enumerate(S_list) if s]
     for nwg in (1, 2, 5, 256):
         out = balanced(case, nwg=nwg).float().cpu()
@@ -91,18 +106,22 @@ def test_balanced_zero_length_requests(gpu):
         assert_close(out[live].numpy(), oracle(case, SCALE, live), ATOL, RTOL, f"zero/nwg{nwg}")
 
 
-def test_balanced_many_requests(gpu):
-    # More requests than one 256-thread prefix-scan round, short and ragged.
+@pytest.mark.parametrize("hkv", [8, 16])
+def test_balanced_many_requests(gpu, hkv):
+    # More requests than one prefix-scan round of the workgroup, short and
+    # ragged.
     g = np.random.default_rng(3)
     S_list = [int(x) for x in g.integers(1, 300, size=700)]
-    case = make_case(S_list, 32, 8, 16, pool_factor=1.2, seed=6, qkv_std=0.5, poison=True)
+    case = make_case(S_list, 4 * hkv, hkv, 16, pool_factor=1.2, seed=6, qkv_std=0.5,
+                     poison=True)
     out = balanced(case)
     batches = list(range(0, 700, 7)) + [699]
     assert_close(out[batches], oracle(case, SCALE, batches), ATOL, RTOL, "many")
 
 
-def test_balanced_repeatable(gpu):
-    cfg = dict(S_list=[5000, 1, 2000, 777, 3333, 64], Hq=32, Hkv=8, bs=16)
+@pytest.mark.parametrize("hkv", [8, 16])
+def test_balanced_repeatable(gpu, hkv):
+    cfg = dict(S_list=[5000, 1, 2000, 777, 3333, 64], Hq=4 * hkv, Hkv=hkv, bs=16)
     case = ref_case(cfg, seed=9)
     first = balanced(case)
     for _ in range(3):
@@ -128,9 +147,10 @@ def test_balanced_configs(gpu, name):
     torch.cuda.empty_cache()
 
 
-def test_balanced_parts_equal_launch(gpu):
+@pytest.mark.parametrize("hkv", [8, 16])
+def test_balanced_parts_equal_launch(gpu, hkv):
     # Partial then merge, as two calls, is the combined launch.
-    cfg = dict(S_list=[3000, 17, 900, 2500], Hq=32, Hkv=8, bs=16)
+    cfg = dict(S_list=[3000, 17, 900, 2500], Hq=4 * hkv, Hkv=hkv, bs=16)
     case = ref_case(cfg, seed=12)
     assert torch.equal(balanced(case, parts=True), balanced(case))
 
