@@ -191,8 +191,10 @@ GQA_DECODE_API int gqa_decode_balanced_merge_launch(
  * most 4 q-heads: a longest sequence of at least 6144 tokens, at least 32 MiB
  * of KV, at most 16 (request, kv-head) segments per CU, and not a split grid
  * of exactly one wave per SIMD with at most 8 splits (which uniform lengths
- * make perfectly even). Groups of 5-16 q-heads over 4 or 8 kv-heads: at least
- * 8 requests and 512 MiB of KV. This is the choice the torch op makes for
+ * make perfectly even), and at least 8 requests when there are 4 or 8
+ * kv-heads (the balanced launch then cuts whole requests into pieces). Groups
+ * of 5-16 q-heads over 4 or 8 kv-heads: at least 8 requests and 512 MiB of
+ * KV. This is the choice the torch op makes for
  * num_splits=0. Pure host code. No reference counterpart. */
 GQA_DECODE_API int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size,
                                               int max_blocks, int num_cus);

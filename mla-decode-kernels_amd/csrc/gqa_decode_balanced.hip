@@ -649,6 +649,11 @@ extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size
   // vs 1536; B=8: 100 vs 140); with fewer requests each is cut into many
   // pieces and the merge costs more (B=1 S=32768: 81 vs 36 us; B=8 S=8192: 59
   // vs 51), so below either bound the split launch runs.
+  // Groups of at most 4 over 4 or 8 kv-heads run the matrix-core scan too, on
+  // whole requests, so they take the same batch bound on top of their own rule:
+  // one request cut into a piece per CU loses (32Q/8KV B=1: S=8192 67.5 vs
+  // 21.0 us, S=32768 81.7 vs 34.8), while at B >= 32 with long sequences the
+  // balanced launch wins by 3-6 % (B=128 S=8192: 641 vs 667 us).
   constexpr int64_t kMinLongest = 6144;
   constexpr int64_t kMinBytes = int64_t(32) << 20;
   constexpr int kMaxSegmentsPerCu = 16;
@@ -668,6 +673,7 @@ extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size
     return B >= kMfmaMinBatch && kv_bytes >= kMfmaMinBytes ? 1 : 0;
   }
   if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31)) return 0;
+  if (gqa::mfma_slot_shape(Hkv, G) && B < kMfmaMinBatch) return 0;
   if (s_cap < kMinLongest || kv_bytes < kMinBytes) return 0;
   if ((int64_t)B * Hkv > (int64_t)kMaxSegmentsPerCu * num_cus) return 0;
   const int ns = gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus);

@@ -252,18 +252,35 @@ def test_prefer_balanced_headline_shapes():
                                         (32, 64, 64, 512), (8, 64, 16, 2048), (8, 64, 16, 512),
                                         (7, 64, 64, 2048), (16, 64, 16, 512), (16, 64, 16, 511),
                                         (128, 64, 16, 128), (4, 128, 64, 512), (64, 40, 16, 512)])
-def test_prefer_balanced_rule(B, Hq, bs, mb):
-    # The documented rule, clause by clause.
-    Hkv, cus = 8, 256
+@pytest.mark.parametrize("Hkv", [8, 4, 16])
+def test_prefer_balanced_rule(B, Hq, bs, mb, Hkv):
+    # The documented rule, clause by clause. Hq is given for 8 kv-heads; the
+    # same group runs over 4 (matrix-core scan for every group) and 16 (VALU
+    # scan for groups of at most 4, no balanced launch above).
+    G, cus = Hq // 8, 256
+    Hq = G * Hkv
     s_max = mb * bs
     ns = capi.pick_num_splits(B, Hq, Hkv, bs, mb, cus)
     kv_bytes = B * s_max * Hkv * 512
-    if Hq // Hkv >= 5:
-        want = Hq // Hkv <= 16 and B >= 8 and kv_bytes >= 512 << 20
+    mfma_batch = B >= 8 and kv_bytes >= 512 << 20
+    if G >= 5:
+        want = Hkv in (4, 8) and G <= 16 and mfma_batch
     else:
         want = (s_max >= 6144 and kv_bytes >= 32 << 20 and B * Hkv <= 16 * cus
                 and not (B * Hkv * 4 * ns == 4 * cus and ns <= 8))
+        if Hkv in (4, 8):
+            want = want and B >= 8
     assert capi.prefer_balanced(B, Hq, Hkv, bs, mb, cus) == int(want)
+
+
+def test_prefer_balanced_single_request_small_group():
+    # 32Q/8KV, one request of 8192 or 32768 tokens: the matrix-core balanced
+    # scan would cut it into a piece per CU (measured 67.5 vs 21.0 us and 81.7
+    # vs 34.8 us against the split launch), so the split launch runs.
+    assert capi.prefer_balanced(1, 32, 8, 16, 512, 256) == 0
+    assert capi.prefer_balanced(1, 32, 8, 64, 512, 256) == 0
+    # 128 requests of 8192 tokens keep the balanced launch (641 vs 667 us).
+    assert capi.prefer_balanced(128, 32, 8, 16, 512, 256) == 1
 
 
 def test_prefer_balanced_invalid():
