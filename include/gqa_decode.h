@@ -115,6 +115,42 @@ GQA_DECODE_API int gqa_decode_v2_merge_launch(const float* ws_acc, const float* 
  * workspace inline at python/gqa_decode_ext.cpp:106-109). */
 GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits);
 
+/* Single-launch split-KV: gqa_decode_v2_launch's result in one kernel launch.
+ * The partial kernel runs with the same split rule and layout; the last
+ * workgroup of each merge group (a request's q-heads on one kv-head) to
+ * finish its split folds the group's states in split order with the merge
+ * kernel's arithmetic, so out is bitwise equal to gqa_decode_v2_launch's with
+ * the same num_splits. workspace (16-byte aligned, workspace_bytes at least
+ * gqa_decode_v2_fused_workspace_bytes) starts with B*Hq 32-bit arrival
+ * counters and ends with the v2 workspace (ws_acc, ws_m, ws_l back to back,
+ * as gqa_decode_v2_launch takes them), placed at the last 256-byte boundary
+ * that leaves room for it. The counters must be zero before the first launch
+ * (gqa_decode_v2_fused_reset for the largest B*Hq the workspace will serve);
+ * every launch leaves them zero, so one workspace serves any smaller batch
+ * afterwards. Launches that share a workspace must not overlap (stream order
+ * suffices). No workgroup waits on another. num_splits == 1 runs the
+ * single-pass kernel. No reference counterpart: the reference's v2 is a
+ * partial and a merge launch (kernels/gqa_decode/v2_splitkv.cu:110-125) and
+ * lists the fused merge as a follow-up (README.md:386-387, 410-412). */
+GQA_DECODE_API int gqa_decode_v2_fused_launch(const uint16_t* q, const uint16_t* k_cache,
+                                              const uint16_t* v_cache, const int* block_table,
+                                              const int* seq_lens, uint16_t* out, int B, int Hq,
+                                              int Hkv, int block_size, int max_blocks,
+                                              float scale, int num_splits, void* workspace,
+                                              size_t workspace_bytes, hipStream_t stream);
+
+/* Bytes of workspace gqa_decode_v2_fused_launch needs: 4*B*Hq rounded up to
+ * a multiple of 256, plus gqa_decode_v2_workspace_bytes(B, Hq, num_splits); 0
+ * for non-positive arguments. */
+GQA_DECODE_API size_t gqa_decode_v2_fused_workspace_bytes(int B, int Hq, int num_splits);
+
+/* Zero the arrival counters of a fused-launch workspace for (B, Hq) -- the
+ * first 4*B*Hq bytes, rounded up to 256 -- with a fill kernel on stream (no
+ * memset node, so it can be captured in a graph). Call once after allocating
+ * the workspace. num_splits only sizes the workspace check. */
+GQA_DECODE_API int gqa_decode_v2_fused_reset(void* workspace, size_t workspace_bytes, int B,
+                                             int Hq, int num_splits, hipStream_t stream);
+
 /* Split count that fills the device. Groups of 5-16 q-heads over 4 or 8
  * kv-heads: one workgroup of Hkv waves per CU (B * Hkv * splits = 8 * CUs,
  * rounded down), no split longer than 4096 tokens nor shorter than 1024, at

@@ -6,6 +6,7 @@
 // in gqa_decode_split.hip.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
+#include "gqa_merge.hpp"
 #include "gqa_scan.hpp"
 #include "gqa_scan_mfma.hpp"
 
@@ -66,11 +67,12 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_mfma_kernel(const ScanArgs 
       for (int nb = 0; nb < 8; ++nb) {
         if (a.out)
           a.out[bh * kHeadDim + 16 * nb + j] = (uint16_t)f32_to_bf16_bits(finalize(o[nb][e], Le[e]));
-        if (a.ws_acc) a.ws_acc[(bh * ns + split) * kHeadDim + 16 * nb + j] = o[nb][e];
+        if (a.ws_acc)
+          put_state(a.ws_acc + (bh * ns + split) * kHeadDim + 16 * nb + j, o[nb][e], a.counters);
       }
       if (a.ws_acc && j == 0) {
-        a.ws_m[bh * ns + split] = Me[e] * kLn2;
-        a.ws_l[bh * ns + split] = Le[e];
+        put_state(a.ws_m + bh * ns + split, Me[e] * kLn2, a.counters);
+        put_state(a.ws_l + bh * ns + split, Le[e], a.counters);
       }
     }
   } else {
@@ -111,13 +113,24 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_mfma_kernel(const ScanArgs 
       if (a.out) a.out[bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(finalize(A, Lm));
       if (a.ws_acc) {
         const size_t st = bh * ns + split;
-        a.ws_acc[st * kHeadDim + d] = A;
+        put_state(a.ws_acc + st * kHeadDim + d, A, a.counters);
         if (d == 0) {
-          a.ws_m[st] = M * kLn2;
-          a.ws_l[st] = Lm;
+          put_state(a.ws_m + st, M * kLn2, a.counters);
+          put_state(a.ws_l + st, Lm, a.counters);
         }
       }
     }
+  }
+  // Single-launch split mode: the group's last workgroup merges its heads,
+  // four per wave at a time. Slot-group layout: the group is the request and
+  // each wave merges its own kv-head's q-heads; head-strided: the P waves
+  // share the group's (at most 16) q-heads.
+  if (a.counters != nullptr &&
+      arrive_last(a.counters, kSlot ? (size_t)b : (size_t)b * gridDim.x + blockIdx.x, ns)) {
+    const int first = kSlot ? 0 : 4 * ph, step = kSlot ? 4 : 4 * P;
+    for (int h = first; h < nh; h += step)
+      merge_heads4(a.ws_acc, a.ws_m, a.ws_l, a.merge_out, (size_t)b * a.Hq + h0 + h,
+                   min(4, nh - h), ns, lane);
   }
 }
 

@@ -22,9 +22,12 @@
 // bit for bit.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
+#include "gqa_merge.hpp"
 #include "gqa_scan.hpp"
 #include "gqa_scan_valu.hpp"
 #include "gqa_decode.h"
+
+#include <algorithm>
 
 namespace gqa {
 
@@ -77,12 +80,19 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs 
         }
         if (a.ws_acc) {
           const size_t stx = bh * ns + split;
-          float4* dst = reinterpret_cast<float4*>(a.ws_acc + stx * kHeadDim + 8 * c);
-          dst[0] = make_float4(st.acc[h][0], st.acc[h][1], st.acc[h][2], st.acc[h][3]);
-          dst[1] = make_float4(st.acc[h][4], st.acc[h][5], st.acc[h][6], st.acc[h][7]);
+          float* dst = a.ws_acc + stx * kHeadDim + 8 * c;
+          if (a.counters) {
+#pragma unroll
+            for (int d = 0; d < 8; d += 2) store_coherent2(dst + d, st.acc[h][d], st.acc[h][d + 1]);
+          } else {
+            reinterpret_cast<float4*>(dst)[0] =
+                make_float4(st.acc[h][0], st.acc[h][1], st.acc[h][2], st.acc[h][3]);
+            reinterpret_cast<float4*>(dst)[1] =
+                make_float4(st.acc[h][4], st.acc[h][5], st.acc[h][6], st.acc[h][7]);
+          }
           if (c == 0) {
-            a.ws_m[stx] = Mw[h] * kLn2;  // back to natural-log units
-            a.ws_l[stx] = Lw[h];
+            put_state(a.ws_m + stx, Mw[h] * kLn2, a.counters);  // back to natural-log units
+            put_state(a.ws_l + stx, Lw[h], a.counters);
           }
         }
       }
@@ -100,63 +110,31 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs 
       if (a.out) a.out[bh * kHeadDim + d] = (uint16_t)f32_to_bf16_bits(finalize(A, L));
       if (a.ws_acc) {
         const size_t stx = bh * ns + split;
-        a.ws_acc[stx * kHeadDim + d] = A;
+        put_state(a.ws_acc + stx * kHeadDim + d, A, a.counters);
         if (d == 0) {
-          a.ws_m[stx] = M * kLn2;  // back to natural-log units
-          a.ws_l[stx] = L;
+          put_state(a.ws_m + stx, M * kLn2, a.counters);  // back to natural-log units
+          put_state(a.ws_l + stx, L, a.counters);
         }
       }
     }
   }
+  // Single-launch split mode: the group's last workgroup merges its (at most
+  // four) heads, all in wave 0.
+  if (a.counters != nullptr && arrive_last(a.counters, (size_t)b * gridDim.x + blockIdx.x, ns) &&
+      ph == 0)
+    merge_heads4(a.ws_acc, a.ws_m, a.ws_l, a.merge_out, (size_t)b * a.Hq + h0, nh, ns, lane);
 }
 
 // Log-sum-exp merge of the num_splits states of each (b, q-head) in split order
-// (v2_splitkv.cu:92-108): one wave per (b, q-head), lane i owns dims 2i, 2i+1.
-// The lanes find the max together (one split each), then the splits are folded
-// in order, their states loaded kBatch at a time so the loads overlap.
+// (v2_splitkv.cu:92-108): one wave per (b, q-head) (merge_head).
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(const float* __restrict__ ws_acc,
                                                                const float* __restrict__ ws_m,
                                                                const float* __restrict__ ws_l,
                                                                uint16_t* __restrict__ out, int BH,
                                                                int ns) {
-  constexpr int kBatch = 8;
   const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
   if (bh >= BH) return;
-  const size_t st0 = (size_t)bh * ns;
-  float mloc = kNegInf;
-  for (int i = lane; i < ns; i += 64) mloc = fmaxf(mloc, ws_m[st0 + i]);
-  const float M = wave_max(mloc);
-  float L = 0.f, A0 = 0.f, A1 = 0.f;
-  for (int i0 = 0; i0 < ns; i0 += kBatch) {
-    float mi[kBatch], li[kBatch];
-    float2 av[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const size_t st = st0 + min(i0 + k, ns - 1);  // past the end: a valid split, not folded
-      mi[k] = ws_m[st];
-      li[k] = ws_l[st];
-      av[k] = reinterpret_cast<const float2*>(ws_acc + st * kHeadDim)[lane];
-    }
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      if (i0 + k >= ns) break;
-      // Exactly 1 for the split holding the max, so one split is a no-op merge.
-      const float f = mi[k] == M ? 1.f : exp2_fast((mi[k] - M) * kLog2e);
-      if (i0 + k == 0) {
-        L = li[k] * f;
-        A0 = av[k].x * f;
-        A1 = av[k].y * f;
-      } else {
-        L = fmaf(li[k], f, L);
-        A0 = fmaf(av[k].x, f, A0);
-        A1 = fmaf(av[k].y, f, A1);
-      }
-    }
-  }
-  const uint32_t lo = f32_to_bf16_bits(finalize(A0, L));
-  const uint32_t hi = f32_to_bf16_bits(finalize(A1, L));
-  reinterpret_cast<uint32_t*>(out + (size_t)bh * kHeadDim)[lane] = lo | (hi << 16);
+  merge_head(ws_acc, ws_m, ws_l, out, (size_t)bh, ns, threadIdx.x & 63);
 }
 
 template <int GH, int P>
@@ -179,7 +157,8 @@ hipError_t launch_scan_gh(const ScanArgs& a, int B, hipStream_t stream) {
 hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                        const int* block_table, const int* seq_lens, uint16_t* out, float* ws_acc,
                        float* ws_m, float* ws_l, int B, int Hq, int Hkv, int block_size,
-                       int max_blocks, float scale, int num_splits, hipStream_t stream) {
+                       int max_blocks, float scale, int num_splits, hipStream_t stream,
+                       uint32_t* counters = nullptr, uint16_t* merge_out = nullptr) {
   ScanArgs a;
   a.q = q;
   a.k_cache = k_cache;
@@ -200,6 +179,8 @@ hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_
   a.num_splits = num_splits;
   a.bs_div = make_fastdiv((uint32_t)block_size);
   a.scale_log2e = (float)((double)scale * 1.4426950408889634);
+  a.counters = counters;
+  a.merge_out = merge_out;
   if (use_mfma(a.G)) return launch_scan_mfma(a, B, stream);
   switch (GH) {
     case 1: return launch_scan_gh<1>(a, B, stream);
@@ -280,6 +261,88 @@ extern "C" int gqa_decode_v2_launch(const uint16_t* q, const uint16_t* k_cache,
 extern "C" size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_splits) {
   if (B <= 0 || Hq <= 0 || num_splits <= 0) return 0;
   return (size_t)B * Hq * num_splits * (gqa::kHeadDim + 2) * sizeof(float);
+}
+
+namespace gqa {
+namespace {
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, size_t n,
+                                                       uint32_t v) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    p[i] = v;
+}
+
+// The fused launch's workspace: one 32-bit arrival counter per (request,
+// q-head) at its start -- enough for every launch layout's merge groups, a
+// group holding at least one q-head -- and the v2 workspace (acc, m, l) at its
+// end, starting at a 256-byte boundary. A workspace reset for the largest
+// batch then serves any smaller one: the smaller launch's counters are a
+// prefix of the zeroed ones, which every launch leaves zero, and its states
+// stay clear of them.
+struct FusedWorkspace {
+  uint32_t* counters;
+  float* acc;
+  float* m;
+  float* l;
+};
+
+size_t fused_counter_bytes(int B, int Hq) { return ((size_t)B * Hq * 4 + 255) & ~(size_t)255; }
+
+hipError_t fused_workspace(void* workspace, size_t workspace_bytes, int B, int Hq, int num_splits,
+                           FusedWorkspace& w) {
+  if (num_splits < 1 || num_splits > GQA_DECODE_MAX_SPLITS) return hipErrorInvalidValue;
+  if (!workspace || ((uintptr_t)workspace & 15) != 0) return hipErrorInvalidValue;
+  if (workspace_bytes < gqa_decode_v2_fused_workspace_bytes(B, Hq, num_splits))
+    return hipErrorInvalidValue;
+  const size_t states = (size_t)B * Hq * num_splits;
+  const size_t state_off = (workspace_bytes - states * (kHeadDim + 2) * 4) & ~(size_t)255;
+  w.counters = static_cast<uint32_t*>(workspace);
+  w.acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + state_off);
+  w.m = w.acc + states * kHeadDim;
+  w.l = w.m + states;
+  return hipSuccess;
+}
+
+}  // namespace
+}  // namespace gqa
+
+extern "C" size_t gqa_decode_v2_fused_workspace_bytes(int B, int Hq, int num_splits) {
+  const size_t states = gqa_decode_v2_workspace_bytes(B, Hq, num_splits);
+  return states ? gqa::fused_counter_bytes(B, Hq) + states : 0;
+}
+
+extern "C" int gqa_decode_v2_fused_reset(void* workspace, size_t workspace_bytes, int B, int Hq,
+                                         int num_splits, hipStream_t stream) {
+  if (B < 0 || Hq < 1 || (int64_t)B * Hq > (int64_t(1) << 30)) return hipErrorInvalidValue;
+  if (B == 0) return hipSuccess;
+  gqa::FusedWorkspace w;
+  const hipError_t err = gqa::fused_workspace(workspace, workspace_bytes, B, Hq, num_splits, w);
+  if (err != hipSuccess) return err;
+  const size_t n = gqa::fused_counter_bytes(B, Hq) / 4;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(gqa::fill_u32_kernel, dim3(blocks), dim3(256), 0, stream, w.counters, n, 0u);
+  return hipGetLastError();
+}
+
+extern "C" int gqa_decode_v2_fused_launch(const uint16_t* q, const uint16_t* k_cache,
+                                          const uint16_t* v_cache, const int* block_table,
+                                          const int* seq_lens, uint16_t* out, int B, int Hq,
+                                          int Hkv, int block_size, int max_blocks, float scale,
+                                          int num_splits, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
+  hipError_t err = gqa::check_common(q, k_cache, v_cache, block_table, seq_lens, out, B, Hq, Hkv,
+                                     block_size, max_blocks);
+  if (err != hipSuccess) return err;
+  if (B == 0) return hipSuccess;
+  gqa::FusedWorkspace w;
+  err = gqa::fused_workspace(workspace, workspace_bytes, B, Hq, num_splits, w);
+  if (err != hipSuccess) return err;
+  if (num_splits == 1)  // the single-pass kernel, as gqa_decode_v2_launch runs it
+    return gqa::launch_scan(q, k_cache, v_cache, block_table, seq_lens, out, w.acc, w.m, w.l, B,
+                            Hq, Hkv, block_size, max_blocks, scale, 1, stream);
+  return gqa::launch_scan(q, k_cache, v_cache, block_table, seq_lens, nullptr, w.acc, w.m, w.l, B,
+                          Hq, Hkv, block_size, max_blocks, scale, num_splits, stream, w.counters,
+                          out);
 }
 
 // Number of splits. For the matrix-core scan's slot-group layout (groups of

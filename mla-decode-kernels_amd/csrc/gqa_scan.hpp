@@ -22,6 +22,10 @@ struct ScanArgs {
   int Hq, Hkv, G, nchunk, block_size, max_blocks, num_splits;
   FastDiv bs_div;
   float scale_log2e;  // scale * log2(e): scores are kept in base-2 units
+  // Single-launch split mode: one arrival counter per merge group (zero on
+  // entry, left zero), and the output the group's last workgroup writes.
+  uint32_t* counters = nullptr;
+  uint16_t* merge_out = nullptr;
 };
 
 // GQA groups of at least this many q-heads run the matrix-core scan

@@ -52,6 +52,12 @@ def lib():
         L.gqa_decode_v2_merge_launch.restype = _i
         L.gqa_decode_v2_workspace_bytes.argtypes = [_i, _i, _i]
         L.gqa_decode_v2_workspace_bytes.restype = ctypes.c_size_t
+        L.gqa_decode_v2_fused_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
+        L.gqa_decode_v2_fused_launch.restype = _i
+        L.gqa_decode_v2_fused_workspace_bytes.argtypes = [_i, _i, _i]
+        L.gqa_decode_v2_fused_workspace_bytes.restype = ctypes.c_size_t
+        L.gqa_decode_v2_fused_reset.argtypes = [_vp, ctypes.c_size_t, _i, _i, _i, _vp]
+        L.gqa_decode_v2_fused_reset.restype = _i
         L.gqa_decode_pick_num_splits.argtypes = [_i, _i, _i, _i, _i, _i]
         L.gqa_decode_pick_num_splits.restype = _i
         L.gqa_decode_balanced_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
@@ -90,6 +96,18 @@ def v2_merge_launch(*args):
 
 def workspace_bytes(B, Hq, num_splits):
     return lib().gqa_decode_v2_workspace_bytes(B, Hq, num_splits)
+
+
+def v2_fused_launch(*args):
+    return lib().gqa_decode_v2_fused_launch(*args)
+
+
+def fused_workspace_bytes(B, Hq, num_splits):
+    return lib().gqa_decode_v2_fused_workspace_bytes(B, Hq, num_splits)
+
+
+def v2_fused_reset(*args):
+    return lib().gqa_decode_v2_fused_reset(*args)
 
 
 def pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus):

@@ -23,7 +23,9 @@ def test_library_exports_every_declared_function():
     assert declared == sorted([
         "gqa_decode_v0_launch", "gqa_decode_v1_launch", "gqa_decode_v2_launch",
         "gqa_decode_v2_partial_launch", "gqa_decode_v2_merge_launch",
-        "gqa_decode_v2_workspace_bytes", "gqa_decode_pick_num_splits",
+        "gqa_decode_v2_workspace_bytes", "gqa_decode_v2_fused_launch",
+        "gqa_decode_v2_fused_workspace_bytes", "gqa_decode_v2_fused_reset",
+        "gqa_decode_pick_num_splits",
         "gqa_decode_balanced_launch", "gqa_decode_balanced_workspace_bytes",
         "gqa_decode_balanced_partial_launch", "gqa_decode_balanced_merge_launch",
         "gqa_decode_prefer_balanced",
@@ -176,6 +178,50 @@ def test_v2_rejects_missing_workspace(which):
     ws[which] = None
     assert capi.v2_launch(*launch_args(), 8, *ws, None) == INVALID
     assert capi.v2_merge_launch(*ws, FAKE, 2, 32, 8, None) == INVALID
+
+
+@pytest.mark.parametrize("B,Hq,ns", [(32, 32, 8), (1, 32, 1), (128, 64, 512), (3, 5, 7),
+                                     (1, 1, 1)])
+def test_fused_workspace_bytes(B, Hq, ns):
+    # Arrival counters (4 bytes per (request, q-head), padded to 256 bytes)
+    # first, then the v2 workspace.
+    counters = (4 * B * Hq + 255) // 256 * 256
+    assert capi.fused_workspace_bytes(B, Hq, ns) == counters + capi.workspace_bytes(B, Hq, ns)
+
+
+@pytest.mark.parametrize("args", [(0, 32, 8), (32, 0, 8), (32, 32, 0), (-1, 32, 8)])
+def test_fused_workspace_bytes_invalid(args):
+    assert capi.fused_workspace_bytes(*args) == 0
+
+
+def fused_args(ns=8, ws=FAKE, ws_bytes=None, **over):
+    a = launch_args(**over)
+    if ws_bytes is None:
+        ws_bytes = capi.fused_workspace_bytes(max(a[6], 1), max(a[7], 1), max(ns, 1))
+    return a + [ns, ws, ws_bytes, None]
+
+
+@pytest.mark.parametrize("over", BAD)
+def test_fused_rejects_bad_arguments(over):
+    assert capi.v2_fused_launch(*fused_args(**over)) == INVALID
+
+
+def test_fused_rejects_bad_workspace():
+    # Split counts out of range, a missing, misaligned or short workspace.
+    for ns in (0, -1, 513):
+        assert capi.v2_fused_launch(*fused_args(ns=ns, ws_bytes=1 << 30)) == INVALID
+    assert capi.v2_fused_launch(*fused_args(ws=None)) == INVALID
+    assert capi.v2_fused_launch(*fused_args(ws=FAKE + 4)) == INVALID
+    need = capi.fused_workspace_bytes(2, 32, 8)
+    assert capi.v2_fused_launch(*fused_args(ws_bytes=need - 1)) == INVALID
+    # The reset checks the same workspace rules before launching its fill.
+    for args in [(None, need, 2, 32, 8), (FAKE + 4, need, 2, 32, 8), (FAKE, need - 1, 2, 32, 8),
+                 (FAKE, need, 2, 32, 0), (FAKE, need, -1, 32, 8), (FAKE, need, 2, 0, 8)]:
+        assert capi.v2_fused_reset(*args, None) == INVALID
+    # Empty batches launch nothing.
+    assert capi.v2_fused_reset(None, 0, 0, 32, 8, None) == capi.HIP_SUCCESS
+    assert capi.v2_fused_launch(*fused_args(B=0, q=None, k=None, v=None, bt=None, sl=None,
+                                            out=None, ws=None)) == capi.HIP_SUCCESS
 
 
 @pytest.mark.parametrize("Hq,Hkv,nwg,gh", [(32, 8, 256, 4), (8, 8, 256, 1), (16, 8, 7, 2),
