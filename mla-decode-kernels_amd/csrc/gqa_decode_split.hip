@@ -42,8 +42,9 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs 
   const int ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane >> 4;  // DPP row: token 4j + r of each load j
   const int c = lane & 15;  // dims [8c, 8c + 8)
-  const int hkv = blockIdx.x / a.nchunk;
-  const int hc = blockIdx.x - hkv * a.nchunk;
+  const int hx = blockIdx.x / a.nchunk;
+  const int hkv = strided_kv_head(hx, a.Hkv);
+  const int hc = blockIdx.x - hx * a.nchunk;
   const int b = blockIdx.y, split = blockIdx.z;
   const int h0 = hkv * a.G + hc * GH;  // first q-head of this wave
   const int nh = min(GH, a.G - hc * GH);

@@ -28,6 +28,21 @@ struct ScanArgs {
   uint16_t* merge_out = nullptr;
 };
 
+// The kv-head a head-strided VALU-scan workgroup serves, from its grid
+// position x: adjacent heads swapped when Hkv is even. Workgroups are dealt
+// round-robin to the 8 XCDs by linear id, and with an even grid x extent the
+// XCD number has the parity of x; a head's 256-byte rows have address bit 8
+// equal to the head's parity. On MI355X the VALU scan's gather streams faster
+// when each XCD reads heads of the other parity (probe, 1 GiB: 154.5 us
+// against 161 us; config 2: 164.3 vs 166.2 us, config 3: 165.6 vs 169.2). The
+// matrix-core scan's head-strided launch, which loads K in 64-byte row
+// pieces, was 1-2 % slower with the swap and keeps the plain order. The swap
+// only changes which workgroup computes a (request, kv-head) pair, not how, so
+// results are unchanged bit for bit.
+__device__ __forceinline__ int strided_kv_head(int x, int Hkv) {
+  return (Hkv & 1) ? x : (x ^ 1);
+}
+
 // GQA groups of at least this many q-heads run the matrix-core scan
 // (gqa_scan_mfma.hpp): its VALU work per tile does not grow with the group,
 // while the VALU scan's does (measured: 8-head groups are VALU-bound on the
