@@ -167,14 +167,19 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_balanced_kernel(const ScanA
     const int lt0 = t - seg0;
     const int lt1 = min(t1, seg0 + n) - seg0;
     const int S = clamped_len(a, b, ba.s_cap);
-    const int h0 = hkv * G;
+    // The segment's kv-head: adjacent heads swapped, as in the split grid
+    // (strided_kv_head), so a share whose segment index matches its
+    // workgroup's XCD parity reads heads of the other parity (64Q/16KV, B=16,
+    // S=8192: 172.0 -> 167.1 us).
+    const int kvh = strided_kv_head(hkv, Hkv);
+    const int h0 = kvh * G;
 
     uint4 qf[GH];
     load_q(a, b, h0, G, c, qf);
     WaveState<GH> st;
     init_state(st);
     scan_segment<GH, P, DEPTH, kBlockUniform, true>(a, a.block_table + (size_t)b * a.max_blocks,
-                                                    hkv, qf, kTile * lt0, min(S, kTile * lt1), ph,
+                                                    kvh, qf, kTile * lt0, min(S, kTile * lt1), ph,
                                                     r, c, st);
     float Mw[GH], Lw[GH];
     merge_rows(st, Mw, Lw);
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_balanced_kernel(const ScanA
     // segment if the piece ends early, and is the segment's first cut (where
     // the merge starts) if the piece also starts at the segment's start.
     if (threadIdx.x == 0 && seg0 + lt1 >= t1)
-      ba.meta[w] = ShareMeta{T, seg0, seg0 + n, b, hkv, lt0 == 0 && lt1 < n, 0, 0};
+      ba.meta[w] = ShareMeta{T, seg0, seg0 + n, b, kvh, lt0 == 0 && lt1 < n, 0, 0};
     t = seg0 + lt1;
     if (++hkv == Hkv) {
       hkv = 0;

@@ -28,8 +28,9 @@ struct ScanArgs {
   uint16_t* merge_out = nullptr;
 };
 
-// The kv-head a head-strided VALU-scan workgroup serves, from its grid
-// position x: adjacent heads swapped when Hkv is even. Workgroups are dealt
+// The kv-head a head-strided VALU-scan workgroup (or a token-balanced VALU
+// segment) serves, from its grid position (segment ordinal) x: adjacent
+// heads swapped when Hkv is even. Workgroups are dealt
 // round-robin to the 8 XCDs by linear id, and with an even grid x extent the
 // XCD number has the parity of x; a head's 256-byte rows have address bit 8
 // equal to the head's parity. On MI355X the VALU scan's gather streams faster
