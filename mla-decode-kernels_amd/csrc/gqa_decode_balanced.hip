@@ -23,6 +23,12 @@
 // measured fastest. Lengths are clamped to max_blocks * block_size, so no
 // block-table read leaves the request's row; a request of length 0 gets NaN,
 // as 0/0 gives in the other kernels (and the reference).
+//
+// With 4 or 8 kv-heads (every group of up to 16 q-heads) the matrix-core
+// variant below runs instead: a segment is a whole request (T = sum_b
+// ceil(S_b / 16)), a workgroup holds one wave per kv-head, and every wave
+// scans each piece of its share for its own kv-head with the MFMA scan of
+// gqa_scan_mfma.hpp, so one CU reads each cache slot whole.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
 #include "gqa_scan.hpp"

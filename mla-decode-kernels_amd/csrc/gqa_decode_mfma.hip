@@ -1,9 +1,10 @@
 // Single-pass / split-KV partial scan on the gfx950 matrix cores, used for
-// GQA groups of 5-16 q-heads: the per-tile work is the MFMA scan of
-// gqa_scan_mfma.hpp; this file holds the split-rule kernel and its launches.
+// GQA groups of 5 or more q-heads (16 per MFMA column block, larger groups in
+// chunks of 16): the per-tile work is the MFMA scan of gqa_scan_mfma.hpp;
+// this file holds the split-rule kernel and its launches.
 //
 // Same split rule, workspace contract and fixed-order merges as the VALU scan
-// in gqa_decode_split.hip.
+// in gqa_decode_split.hip, including the single-launch mode.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
 #include "gqa_merge.hpp"
