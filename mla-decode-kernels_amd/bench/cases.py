@@ -110,6 +110,69 @@ def make_config_case(name, seed=0, device="cuda", poison=False, shuffle=True):
                      poison=poison, shuffle=shuffle)
 
 
+# MLA decode workloads: the FlashMLA benchmark rows the reference keeps as its
+# K2 baseline (docs/g0/flashmla_bench_raw.txt:4674-4719 of the reference):
+# b=128, h_q=128, one latent head, d=576, dv=512, block 64, varlen lengths
+# around s_k, s_q = 1 (plain decode) or 2 (two query tokens per request).
+MLA_CONFIGS = {
+    f"mla_{sk // 1024}k" + ("_sq2" if sq == 2 else ""): dict(B=128, s_q=sq, h_q=128, S_mean=sk,
+                                                              bs=64, causal=False)
+    for sq in (1, 2) for sk in (4096, 8192, 16384, 32768)
+}
+
+
+def mla_seq_lens(B, S_mean, seed=0, s_q=1):
+    """FlashMLA's varlen draw, seeded: max(N(S_mean, S_mean / 2), s_q) per
+    request, on a CPU generator so that every machine builds the same batch."""
+    g = torch.Generator().manual_seed(seed + 7)
+    x = torch.randn(B, generator=g, dtype=torch.float64) * (S_mean / 2) + S_mean
+    return [max(int(v), s_q) for v in x.tolist()]
+
+
+def make_mla_case(S_list, s_q, h_q, bs, *, pool=None, pool_factor=None, seed=0, device="cuda",
+                  std=1.0, poison=False, shuffle=True):
+    """(q [B, s_q, h_q, 576], kv_cache [pool, bs, 1, 576], block_table, seq_lens)
+    on `device`, as make_case builds the GQA cases: seeded N(0, std^2) bf16,
+    a shuffled pool, -1 past each request's blocks, and with poison=True NaN
+    in every cache slot no request owns (including the tail of each last
+    block)."""
+    B = len(S_list)
+    D = 576
+    n_blocks = [(int(x) + bs - 1) // bs for x in S_list]
+    needed = sum(n_blocks)
+    if pool is None:
+        pool = max(1, math.ceil(needed * pool_factor) if pool_factor else needed)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = (torch.randn(B, s_q, h_q, D, device=device, generator=gen) * std).to(torch.bfloat16)
+    kv = torch.empty(pool, bs, 1, D, device=device, dtype=torch.bfloat16)
+    slab = max(1, (64 << 20) // (bs * D))
+    for i in range(0, pool, slab):
+        n = min(slab, pool - i)
+        kv[i:i + n] = (torch.randn(n, bs, 1, D, device=device, generator=gen) * std).to(
+            torch.bfloat16)
+    perm = (torch.randperm(pool, generator=torch.Generator().manual_seed(seed)) if shuffle
+            else torch.arange(pool))
+    max_blocks = max(max(n_blocks), 1) if n_blocks else 1
+    block_table = torch.full((B, max_blocks), -1, dtype=torch.int32)
+    used = torch.zeros(pool, dtype=torch.bool)
+    off = 0
+    for b in range(B):
+        ids = perm[off:off + n_blocks[b]]
+        block_table[b, :n_blocks[b]] = ids.to(torch.int32)
+        used[ids] = True
+        off += n_blocks[b]
+    if poison:
+        unused = (~used).nonzero().flatten().to(device)
+        if unused.numel():
+            kv.index_fill_(0, unused, float("nan"))
+        for b in range(B):
+            rem = int(S_list[b]) % bs
+            if rem:
+                kv[int(block_table[b, n_blocks[b] - 1]), rem:] = float("nan")
+    seq_lens = torch.tensor([int(x) for x in S_list], dtype=torch.int32, device=device)
+    return q, kv, block_table.to(device), seq_lens
+
+
 def kv_bytes(S_list, Hkv):
     """Algorithmic K+V bytes of one decode step: sum_b S_b * Hkv * 128 * 2 * 2
     (bench/common.py:67-69 of the reference, per request)."""

@@ -29,7 +29,7 @@ ARCH = "gfx950"
 
 KERNEL_LIB = os.path.join(LIB_DIR, "libgqa_decode_hip.so")
 HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip", "gqa_decode_mfma.hip",
-               "gqa_decode_balanced.hip"]
+               "gqa_decode_balanced.hip", "mla_decode.hip"]
 # Packed fp32 VALU ops are disabled for all device code.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",

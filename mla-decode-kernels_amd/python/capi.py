@@ -14,6 +14,7 @@ import re
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_DIR, "lib", "libgqa_decode_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "gqa_decode.h")
+MLA_HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "mla_decode.h")
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
@@ -25,12 +26,18 @@ _LAUNCH_ARGS = [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_float
 _lib = None
 
 
-def declared_functions():
-    """Names of the functions include/gqa_decode.h declares."""
-    with open(HEADER_PATH) as f:
+def declared_functions(header=None, prefix="gqa_decode_"):
+    """Names of the functions a header of include/ declares (default:
+    include/gqa_decode.h)."""
+    with open(header or HEADER_PATH) as f:
         text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
-    pat = r"^\s*(?:GQA_DECODE_API\s+)?(?:int|size_t)\s+(gqa_decode_\w+)\s*\("
+    pat = r"^\s*(?:GQA_DECODE_API\s+)?(?:int|size_t)\s+(" + prefix + r"\w+)\s*\("
     return sorted(set(re.findall(pat, text, flags=re.M)))
+
+
+def declared_mla_functions():
+    """Names of the functions include/mla_decode.h declares."""
+    return declared_functions(MLA_HEADER_PATH, "mla_decode_")
 
 
 def lib():
@@ -70,6 +77,13 @@ def lib():
             fn.restype = _i
         L.gqa_decode_prefer_balanced.argtypes = [_i, _i, _i, _i, _i, _i]
         L.gqa_decode_prefer_balanced.restype = _i
+        L.mla_decode_launch.argtypes = [_vp] * 6 + [_i] * 5 + [ctypes.c_float, _i, _i, _vp,
+                                                                ctypes.c_size_t, _vp]
+        L.mla_decode_launch.restype = _i
+        L.mla_decode_workspace_bytes.argtypes = [_i] * 4
+        L.mla_decode_workspace_bytes.restype = ctypes.c_size_t
+        L.mla_decode_pick_num_splits.argtypes = [_i] * 6
+        L.mla_decode_pick_num_splits.restype = _i
         _lib = L
     return _lib
 
@@ -132,3 +146,15 @@ def balanced_merge_launch(*args):
 
 def prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus):
     return lib().gqa_decode_prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus)
+
+
+def mla_launch(*args):
+    return lib().mla_decode_launch(*args)
+
+
+def mla_workspace_bytes(B, s_q, h_q, num_splits):
+    return lib().mla_decode_workspace_bytes(B, s_q, h_q, num_splits)
+
+
+def mla_pick_num_splits(B, s_q, h_q, block_size, max_blocks, num_cus):
+    return lib().mla_decode_pick_num_splits(B, s_q, h_q, block_size, max_blocks, num_cus)

@@ -40,6 +40,10 @@ def lib():
         L.oracle_partial_state.restype = None
         L.oracle_merge_states.argtypes = [ctypes.c_int, _f64p, _f64p, _f64p, ctypes.c_int, _f64p]
         L.oracle_merge_states.restype = None
+        L.oracle_mla_decode.argtypes = [_u16p, _u16p, _i32p, _i32p, _f32p, _f32p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        L.oracle_mla_decode.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -87,3 +91,23 @@ def merge_states(ms, ls, accs):
     out = np.empty(accs.shape[1], dtype=np.float64)
     lib().oracle_merge_states(len(ms), ms, ls, accs, accs.shape[1], out)
     return out
+
+
+def mla_decode_ref(q, kv_cache, block_table, seq_lens, scale, causal=False, dv=512, nthreads=0):
+    """MLA decode in double precision (oracle/mla_decode_oracle.c):
+    (out [B, s_q, h_q, dv] float32, lse [B, h_q, s_q] float32); bf16 inputs
+    as uint16 arrays of raw bits."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kv_cache = np.ascontiguousarray(kv_cache, dtype=np.uint16)
+    block_table = np.ascontiguousarray(block_table, dtype=np.int32)
+    seq_lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    B, s_q, h_q, _ = q.shape
+    bs = kv_cache.shape[1]
+    out = np.empty((B, s_q, h_q, dv), dtype=np.float32)
+    lse = np.empty((B, h_q, s_q), dtype=np.float32)
+    rc = lib().oracle_mla_decode(q, kv_cache, block_table, seq_lens, out, lse, B, s_q, h_q, bs,
+                                 block_table.shape[1], dv, float(scale), int(bool(causal)),
+                                 int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_mla_decode rejected its arguments or ran out of memory")
+    return out, lse

@@ -384,3 +384,57 @@ def test_op_check_order_and_messages(binding):
         binding.gqa_decode_v2(q.float(), k, v, bt, sl, 0.088, num_splits=4)
     with pytest.raises(TypeError):
         binding.gqa_decode_v2(q, k, v, bt, sl, 0.088, num_splits="x")
+
+
+# ------------------------------------------------------------ MLA decode ABI
+
+
+def test_mla_exports():
+    declared = capi.declared_mla_functions()
+    assert declared == ["mla_decode_launch", "mla_decode_pick_num_splits",
+                        "mla_decode_workspace_bytes"]
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    names = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    assert {n for n in names if n.startswith("mla")} == set(declared)
+
+
+@pytest.mark.parametrize("B,s_q,h_q,ns", [(128, 1, 128, 2), (1, 2, 16, 64), (3, 1, 5, 7)])
+def test_mla_workspace_bytes(B, s_q, h_q, ns):
+    assert capi.mla_workspace_bytes(B, s_q, h_q, ns) == B * s_q * h_q * ns * (512 + 2) * 4
+    assert capi.mla_workspace_bytes(B, s_q, h_q, 1) == 0
+
+
+def test_mla_pick_num_splits():
+    # One workgroup per CU: 128 requests of 128 rows -> 2 splits on 256 CUs;
+    # one long request -> capped by 256-token splits and the 128 maximum.
+    assert capi.mla_pick_num_splits(128, 1, 128, 64, 512, 256) == 2
+    assert capi.mla_pick_num_splits(1, 1, 128, 64, 512, 256) == 128
+    assert capi.mla_pick_num_splits(1, 1, 128, 64, 4, 256) == 1
+    assert capi.mla_pick_num_splits(64, 1, 256, 64, 512, 256) == 2  # two row groups
+    assert capi.mla_pick_num_splits(0, 1, 128, 64, 512, 256) == 0
+
+
+def mla_args(**over):
+    a = dict(q=FAKE, kv=FAKE, bt=FAKE, sl=FAKE, out=FAKE, lse=FAKE, B=2, s_q=1, h_q=16, bs=64,
+             mb=4, scale=0.04, causal=0, ns=1, ws=None, wsb=0)
+    a.update(over)
+    return [a[k] for k in ("q", "kv", "bt", "sl", "out", "lse", "B", "s_q", "h_q", "bs", "mb",
+                           "scale", "causal", "ns", "ws", "wsb")] + [None]
+
+
+@pytest.mark.parametrize("over", [dict(B=-1), dict(B=70000), dict(s_q=0), dict(h_q=0),
+                                  dict(bs=0), dict(mb=0), dict(ns=0), dict(ns=129),
+                                  dict(q=None), dict(kv=None), dict(bt=None), dict(sl=None),
+                                  dict(out=None), dict(ns=4, ws=None, wsb=1 << 20),
+                                  dict(ns=4, ws=FAKE + 4, wsb=1 << 20), dict(ns=4, wsb=16,
+                                                                             ws=FAKE)])
+def test_mla_rejects_bad_arguments(over):
+    assert capi.mla_launch(*mla_args(**over)) == INVALID
+
+
+def test_mla_empty_batch_is_a_no_op():
+    assert capi.mla_launch(*mla_args(B=0, q=None, kv=None, bt=None, sl=None, out=None,
+                                     lse=None)) == capi.HIP_SUCCESS
