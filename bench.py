@@ -46,6 +46,11 @@ sys.path.insert(0, os.path.join(PKG_DIR, "bench"))
 
 METRIC = ("median µs and % of HBM KV-bytes SoL, 32Q/8KV d=128 S=8192 B=32 block=16")
 TRAFFIC_FILE = os.path.join(REPO_ROOT, "profiles", "traffic.txt")
+MLA_NAMES = [f"mla_{k}k{sfx}" for sfx in ("", "_sq2") for k in (4, 8, 16, 32)]
+MLA_METRIC = ("median µs, TFLOP/s and GB/s of MLA absorbed decode (FlashMLA's accounting), "
+              "b=128 h_q=128 h_kv=1 d=576 dv=512 block=64 varlen")
+MFMA_BF16_PEAK = 2.5e15
+HBM_PEAK = 8e12
 
 
 def log(msg):
@@ -57,7 +62,9 @@ def parse_args(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"] + MLA_NAMES,
+                    help="GQA configs c1..c5, or an MLA decode workload (FlashMLA's rows)")
+    ap.add_argument("--causal", action="store_true", help="MLA configs: causal mask")
     ap.add_argument("--kernel", default="v2", choices=["v0", "v1", "v2", "balanced"],
                     help="v2 with --num-splits 0 makes the op's automatic choice (balanced or split)")
     ap.add_argument("--num-splits", type=int, default=0, help="v2 split count (0 = heuristic)")
@@ -131,6 +138,8 @@ def main(argv=None):
                           "median_us": round(ms * 1e3, 2),
                           "gbps_read_plus_write": round(2 * n / ms / 1e6, 1)}), flush=True)
         return 0
+    if args.config in MLA_NAMES:
+        return main_mla(args, dev, props)
     cfg = cases.CONFIGS[args.config]
     S_list = cases.config_seq_lens(args.config, args.seed)
     kvb = cases.kv_bytes(S_list, cfg["Hkv"])
@@ -301,6 +310,191 @@ def main(argv=None):
         result["cpu_baseline"] = cpu_baseline(args, case, out, S_list, scale, median_us)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def main_mla(args, dev, props):
+    """One MLA decode step over a FlashMLA benchmark workload, timed as the GQA
+    steps are: the token-balanced launch (plan, split and merge kernels; one
+    workgroup per CU) by default, or with --num-splits N the fixed-split
+    launch (split kernel, then the combine kernel when N > 1)."""
+    import torch
+
+    import capi
+    import cases
+
+    cfg = cases.MLA_CONFIGS[args.config]
+    B, s_q, h_q, bs = cfg["B"], cfg["s_q"], cfg["h_q"], cfg["bs"]
+    S_list = cases.mla_seq_lens(B, cfg["S_mean"], args.seed, s_q)
+    flops, nbytes = cases.mla_flops_bytes(S_list, s_q, h_q)
+    ridge = MFMA_BF16_PEAK / HBM_PEAK
+    bound = "mfma" if flops / nbytes > ridge else "hbm"
+    sol = max(flops / MFMA_BF16_PEAK, nbytes / HBM_PEAK) * 1e6
+    log(f"config {args.config}: B={B} s_q={s_q} h_q={h_q} sum(S)={sum(S_list)}; "
+        f"{flops / 1e9:.1f} GFLOP, {nbytes / 1e6:.1f} MB; {bound}-bound, SoL {sol:.1f} us")
+    t0 = time.time()
+    case = cases.make_mla_case(S_list, s_q, h_q, bs, seed=args.seed, device=dev)
+    q, kv, bt, sl = case
+    torch.cuda.synchronize()
+    log(f"inputs resident in HBM ({time.time() - t0:.1f}s)")
+    mb = bt.shape[1]
+    scale = 576 ** -0.5
+    cus = props.multi_processor_count
+    balanced = args.num_splits == 0
+    ns = args.num_splits
+    out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, h_q, s_q, dtype=torch.float32, device=dev)
+    wsb = (capi.mla_balanced_workspace_bytes(B, s_q, h_q, cus) if balanced
+           else capi.mla_workspace_bytes(B, s_q, h_q, ns))
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    largs = (q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(), out.data_ptr(),
+             lse.data_ptr(), B, s_q, h_q, bs, mb, scale, int(args.causal),
+             cus if balanced else ns, ws.data_ptr(), wsb, sp)
+    launch = capi.mla_balanced_launch if balanced else capi.mla_launch
+
+    def step():
+        rc = launch(*largs)
+        if rc != 0:
+            raise RuntimeError(f"MLA launch failed: hipError_t {rc}")
+
+    t_ramp = time.perf_counter() + args.ramp_seconds
+    while time.perf_counter() < t_ramp:
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    groups = max(1, min(10, K // 5))
+    bounds = [round(g * K / groups) for g in range(groups + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for g in range(groups):
+        ev[g].record(stream)
+        for _ in range(bounds[g + 1] - bounds[g]):
+            step()
+    ev[groups].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    group_us = sorted(ev[g].elapsed_time(ev[g + 1]) * 1e3 / (bounds[g + 1] - bounds[g])
+                      for g in range(groups))
+    median_us = group_us[groups // 2]
+
+    # The split kernel alone, K launches back to back: its average duration
+    # (fixed splits; the balanced split kernel needs its plan launch first, so
+    # there the whole step stands in, and the rocprofv3 summary splits it).
+    if balanced:
+        kern_us = median_us
+    else:
+        kev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        kev[0].record(stream)
+        for _ in range(K):
+            if capi.mla_splitkv_launch(*largs) != 0:
+                raise RuntimeError("mla_decode_splitkv_launch failed")
+        kev[1].record(stream)
+        torch.cuda.synchronize()
+        kern_us = kev[0].elapsed_time(kev[1]) * 1e3 / K
+    step()  # out and lse of a whole step again, for the spot check
+    torch.cuda.synchronize()
+    tflops_k = flops / kern_us / 1e6
+    gbps_k = nbytes / kern_us / 1e3
+    log(f"mla: median step {median_us:.2f} us (groups {group_us[0]:.1f}..{group_us[-1]:.1f}), "
+        f"split kernel avg {kern_us:.2f} us ({tflops_k:.0f} TFLOP/s, {gbps_k:.0f} GB/s), "
+        f"{'balanced' if balanced else f'num_splits {ns}'}")
+    achieved = tflops_k if bound == "mfma" else gbps_k
+    peak = MFMA_BF16_PEAK / 1e12 if bound == "mfma" else HBM_PEAK / 1e9
+    h100 = cases.MLA_H100_MS.get(args.config)
+    result = {
+        "metric": MLA_METRIC,
+        "value": round(median_us, 3),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / K * 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "accum": "fp32",
+        "data": f"synthetic N(0,1) bf16, seed {args.seed}",
+        "config": {"workload": f"{args.config}: FlashMLA row b={B} s_q={s_q} "
+                               f"s_k={cfg['S_mean']} varlen h_q={h_q} h_kv=1 block={bs}",
+                   "causal": bool(args.causal),
+                   "launch": "balanced" if balanced else f"num_splits={ns}"},
+        "tflops": round(flops / median_us / 1e6, 1),
+        "gbps": round(nbytes / median_us / 1e3, 1),
+        "flops": flops, "bytes": nbytes,
+        "pct_of_sol": round(sol / median_us * 100, 2),
+        "flashmla_h100_us": h100 * 1e3 if h100 else None,
+        "roofline": {"bound": bound,
+                     "kernel": "whole step" if balanced else "mla_decode_kernel",
+                     "achieved": round(achieved, 1),
+                     "peak": peak, "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                     "frac": round(achieved / peak, 4), "avg_kernel_us": round(kern_us, 3),
+                     "mfma_frac": round(tflops_k * 1e12 / MFMA_BF16_PEAK, 4),
+                     "hbm_frac": round(gbps_k * 1e9 / HBM_PEAK, 4), "traffic": None},
+        "device": props.name, "gcn_arch": props.gcnArchName, "cus": props.multi_processor_count,
+        "clocks": cases.gpu_clocks(),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_mla(args, case, out, lse, S_list, scale, median_us)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
+    """The MLA oracle (oracle/mla_decode_oracle.c) on this host's cores over
+    whole requests of the workload (~10 s), scaled to one full step; its output
+    on the sample is compared with the GPU's (out within 2e-2, lse 5e-3)."""
+    import numpy as np
+
+    from cases import mla_host_case
+    sys.path.insert(0, REPO_ROOT)
+    from oracle import c_oracle  # noqa: E402  (the checker, timed as the CPU baseline)
+
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    B = len(S_list)
+    t0 = time.perf_counter()
+    c_oracle.mla_decode_ref(*mla_host_case(case, [0]), scale, causal=args.causal,
+                            nthreads=threads)
+    per_token = (time.perf_counter() - t0) / max(S_list[0], 1)
+    budget_s, sample, tokens = 10.0, [], 0
+    for b in range(B):
+        if sample and (tokens + S_list[b]) * per_token > budget_s:
+            break
+        sample.append(b)
+        tokens += S_list[b]
+    hc = mla_host_case(case, sample)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ref_out, ref_lse = c_oracle.mla_decode_ref(*hc, scale, causal=args.causal,
+                                                   nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    frac = tokens / sum(S_list)
+    cpu_us = t / frac * 1e6
+    got = out[sample].float().cpu().numpy()
+    got_lse = lse[sample].cpu().numpy()
+    err = float(np.abs(got - ref_out).max())
+    lse_err = float(np.abs(got_lse - ref_lse).max())
+    ok = bool(np.allclose(got, ref_out, atol=2e-2, rtol=2e-2)) and lse_err <= 5e-3
+    log(f"cpu baseline: {len(sample)} of {B} requests in {t:.2f}s on {threads} threads -> "
+        f"{cpu_us / 1e3:.1f} ms per full step; spot check max-abs {err:.2e}, lse {lse_err:.2e} "
+        f"{'ok' if ok else 'FAILED'}")
+    if not ok:
+        raise SystemExit("spot check of the GPU output against the oracle failed")
+    return {"value": round(cpu_us, 1), "unit": "us", "cores": threads, "kind": "port",
+            "sample": f"requests {sample[0]}..{sample[-1]} ({len(sample)} of {B}, "
+                      f"{tokens} tokens = {frac * 100:.1f}% of the step), median of 3 runs of "
+                      f"oracle/mla_decode_oracle.c, scaled to the full step",
+            "speedup_gpu_vs_cpu": round(cpu_us / gpu_us, 1),
+            "spot_check_max_abs": err, "spot_check_lse_max_abs": lse_err}
 
 
 def cpu_baseline(args, case, out, S_list, scale, gpu_us):

@@ -69,6 +69,50 @@ GQA_DECODE_API int mla_decode_launch(const uint16_t* q, const uint16_t* kv_cache
                                      int num_splits, void* workspace, size_t workspace_bytes,
                                      hipStream_t stream);
 
+/* The two launches of mla_decode_launch, for a caller that schedules them
+ * itself (or times them apart): the split kernel alone (same arguments; with
+ * num_splits == 1 it writes out and lse, else the workspace states), then the
+ * combine kernel, which folds the num_splits states of every (request, query
+ * row) from the workspace into out and lse (num_splits >= 2; same workspace
+ * and sizes as the split launch). Like FlashMLA's split and combine kernels,
+ * which its single call runs back to back. */
+GQA_DECODE_API int mla_decode_splitkv_launch(const uint16_t* q, const uint16_t* kv_cache,
+                                             const int* block_table, const int* seq_lens,
+                                             uint16_t* out, float* lse, int B, int s_q, int h_q,
+                                             int block_size, int max_blocks, float scale,
+                                             int causal, int num_splits, void* workspace,
+                                             size_t workspace_bytes, hipStream_t stream);
+GQA_DECODE_API int mla_decode_combine_launch(void* workspace, size_t workspace_bytes,
+                                             uint16_t* out, float* lse, int B, int s_q, int h_q,
+                                             int num_splits, hipStream_t stream);
+
+/* Token-balanced MLA decode: the same results as mla_decode_launch (to
+ * rounding), with the batch's work cut into equal shares whatever the lengths,
+ * as FlashMLA's tile scheduler does. The work is every request's 32-token
+ * tiles in request order (T = sum_b ceil(S_b / 32)); each of the ceil(s_q h_q
+ * / 128) row groups gets n = num_workgroups / row groups shares
+ * (num_workgroups <= 0: the device's CU count), share w taking tiles
+ * [w T / n, (w + 1) T / n). Three launches on `stream`: a one-workgroup plan
+ * kernel (tile prefix sums and each share's first request, from seq_lens on
+ * the device: no host synchronisation, graph-capturable), the split kernel
+ * (requests that fall inside one share are written to out and lse directly,
+ * the pieces of the others to workspace states), and a merge of the cut
+ * requests in share order (bitwise reproducible for a given num_workgroups).
+ * workspace: mla_decode_balanced_workspace_bytes(B, s_q, h_q, num_workgroups)
+ * bytes, 16-byte aligned, uninitialised is fine. */
+GQA_DECODE_API int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_cache,
+                                              const int* block_table, const int* seq_lens,
+                                              uint16_t* out, float* lse, int B, int s_q, int h_q,
+                                              int block_size, int max_blocks, float scale,
+                                              int causal, int num_workgroups, void* workspace,
+                                              size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes for mla_decode_balanced_launch (0 for invalid arguments):
+ * two states of s_q * h_q rows x (512 + 2) floats per share, the tile prefix
+ * sums (B + 2 uint64) and the shares' first requests. */
+GQA_DECODE_API size_t mla_decode_balanced_workspace_bytes(int B, int s_q, int h_q,
+                                                          int num_workgroups);
+
 /* Workspace bytes for mla_decode_launch: B * s_q * h_q * num_splits * (512 + 2)
  * * 4 for num_splits > 1, 0 for num_splits == 1 or invalid arguments. */
 GQA_DECODE_API size_t mla_decode_workspace_bytes(int B, int s_q, int h_q, int num_splits);

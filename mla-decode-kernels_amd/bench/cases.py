@@ -173,6 +173,46 @@ def make_mla_case(S_list, s_q, h_q, bs, *, pool=None, pool_factor=None, seed=0, 
     return q, kv, block_table.to(device), seq_lens
 
 
+# FlashMLA's published H100 rows for these workloads (b=128, h_q=128, h_kv=1,
+# block 64, varlen, not causal), ms per call: docs/g0/flashmla_bench_raw.txt
+# of the reference, lines 4675-4697.
+MLA_H100_MS = {"mla_4k": 0.274, "mla_8k": 0.504, "mla_16k": 0.962, "mla_32k": 1.873,
+               "mla_4k_sq2": 0.425, "mla_8k_sq2": 0.805, "mla_16k_sq2": 1.565,
+               "mla_32k_sq2": 3.096}
+
+
+def mla_flops_bytes(seq_lens, s_q, h_q, d=576, dv=512):
+    """FlashMLA's accounting of one decode step, the numbers its benchmark
+    divides by the time: FLOPs of QK^T and PV over every query row and key
+    (2 * s_q * h_q * sum(S) * (d + dv), no causal discount) and bytes of q,
+    the latent rows once and the output (bf16)."""
+    total = float(sum(max(int(x), 0) for x in seq_lens))
+    B = len(seq_lens)
+    flops = 2.0 * s_q * h_q * total * (d + dv)
+    nbytes = (B * s_q * h_q * d + total * d + B * s_q * h_q * dv) * 2
+    return flops, nbytes
+
+
+def mla_host_case(case, batches):
+    """Host (numpy) copy of the listed requests of an MLA case (q, kv_cache,
+    block_table, seq_lens), their blocks compacted into a small pool with
+    remapped ids."""
+    q, kv, bt, sl = case
+    batches = list(batches)
+    bs = kv.shape[1]
+    sl_h = sl.cpu().numpy()[batches]
+    bt_h = bt.cpu().numpy()[batches]
+    n = [(int(x) + bs - 1) // bs for x in sl_h]
+    ids = np.concatenate([bt_h[i, :n[i]] for i in range(len(batches))]).astype(np.int64)
+    new_bt = np.full((len(batches), max(max(n), 1)), -1, dtype=np.int32)
+    off = 0
+    for i in range(len(batches)):
+        new_bt[i, :n[i]] = np.arange(off, off + n[i])
+        off += n[i]
+    pool = kv.index_select(0, torch.from_numpy(ids).to(kv.device))
+    return bits(q[batches]), bits(pool), new_bt, sl_h.astype(np.int32)
+
+
 def kv_bytes(S_list, Hkv):
     """Algorithmic K+V bytes of one decode step: sum_b S_b * Hkv * 128 * 2 * 2
     (bench/common.py:67-69 of the reference, per request)."""

@@ -56,13 +56,11 @@ constexpr int kRowsPerGroup = kWaves * kRowsPerWave;  // 128
 constexpr int kTileBlocks = 2 * kKSteps;              // 36 blocks of 1 KiB
 constexpr int kTileBytes = kTileBlocks * 1024;
 constexpr int kStageLoads = kTileBlocks / kWaves;     // 9 per wave per tile
+// Tiles in the LDS ring: while a tile is consumed, the next kDepth - 1 are in
+// flight from HBM (about 100 KiB per CU, enough to cover the latency at this
+// CU's share of the bandwidth).
+constexpr int kDepth = 4;
 constexpr int kNB = kDV / 16;                         // 32 PV column blocks
-// Q^T k-steps [0, kQLds) live in LDS (one 1 KiB block per 16-row block and
-// k-step), the rest in registers: all 18 in registers would not fit next to
-// the 32 x 512 fp32 accumulators.
-constexpr int kQLds = 9;
-constexpr int kQRegs = kKSteps - kQLds;
-constexpr int kQBlocks = (kRowsPerGroup / 16) * kQLds;  // 72 blocks of 1 KiB
 static_assert(kTileBlocks % kWaves == 0, "staging blocks must split evenly");
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -80,7 +78,9 @@ struct MlaArgs {
   float* ws_acc;  // [B, R, ns, 512]
   float* ws_m;    // [B, R, ns] natural-log units
   float* ws_l;
-  int B, s_q, h_q, R, block_size, max_blocks, num_splits, causal;
+  const uint64_t* pre;  // balanced launch: tile prefix sums [B + 1]
+  const int* first;     // balanced launch: each share's first request
+  int B, s_q, h_q, R, block_size, max_blocks, num_splits, causal, nshare;
   FastDiv bs_div;
   float scale_log2e;
 };
@@ -96,29 +96,100 @@ struct RowState {
   f32x4_t o[kNB];
 };
 
+// A row's probabilities are taken relative to a reference max that is set by
+// the first tile holding a live key of the row and then kept: rescaling the
+// 32 x 512 fp32 accumulators (all 256 accumulation registers of the lane) on
+// every new max would cost more than the tile's matrix work, and any
+// conditional update of them inside the tile loop makes the compiler copy them
+// on every tile. Probabilities stay below 2^kRefSlack; if a later tile beats a
+// row's reference by more, the workgroup runs its split a second time against
+// the rows' true maxima (the values are exact either way; only that split's
+// time doubles).
+constexpr float kRefSlack = 32.f;
+// LDS operand reads run this many MFMA steps ahead of their use: QK k-steps
+// (4 MFMAs each) and PV column blocks (2 MFMAs each).
+constexpr int kQKAhead = 2;
+constexpr int kPVAhead = 4;
+
+// Direct HBM -> LDS copies of 16 bytes per lane (global_load_lds_dwordx4):
+// lane x's bytes land at LDS byte address lds + 16 x; lds must be
+// wave-uniform. They are issued through inline assembly so that the compiler
+// does not tie its LDS reads of the other ring slots to these loads'
+// completion (it would wait for every load in flight before each read);
+// completion is awaited explicitly with s_waitcnt vmcnt before the barrier
+// that publishes a tile. The first form addresses base + voff (a uniform
+// 64-bit base, a 32-bit per-lane offset); the second a per-lane address.
+__device__ __forceinline__ void load_to_lds(const uint16_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+               :
+               : "v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void load_to_lds(const uint16_t* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// Waits until at most kInFlight of this wave's direct loads are outstanding
+// (they complete in issue order), then joins the workgroup barrier; LDS reads
+// and writes are not moved across it.
+template <int kInFlight>
+__device__ __forceinline__ void publish_barrier() {
+  static_assert(kInFlight >= 0 && kInFlight < 64, "vmcnt holds 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(kInFlight) : "memory");
+}
+
+// Max over lanes l, l ^ 16, l ^ 32 and l ^ 48, the four lanes that hold one
+// row in the MFMA C layout: v_permlane16_swap (v_permlane32_swap) with both
+// operands x hands every lane x of itself and of its xor-16 (xor-32) partner,
+// in VALU registers (no LDS round trip).
+__device__ __forceinline__ float row_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
+  const uint32_t v = __builtin_bit_cast(uint32_t, y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__builtin_bit_cast(float, b[0]), __builtin_bit_cast(float, b[1]));
+}
+
+// Where a piece's results go: normalised rows to out and lse (direct), or
+// unnormalised states, row r of the piece's request at index
+// st_base + r * st_stride of ws_acc (x 512), ws_m and ws_l.
+struct PieceOut {
+  bool direct;
+  size_t st_base;
+  int st_stride;
+};
+
+// The workgroup's 128 query rows (row group rg) of request b against tokens
+// [seg_start, seg_end) of the request's S live tokens. Every wave of the
+// workgroup calls it with the same arguments (its barriers are workgroup-wide).
 template <bool kBlockUniform>
-__global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[2][kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t qlds[kQBlocks * 1024];
+__device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTileBytes],
+                                          int* restart_vote, int b, int rg, int S, int seg_start,
+                                          int seg_end, PieceOut po) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const int b = blockIdx.y, split = blockIdx.z;
-  const int row0 = blockIdx.x * kRowsPerGroup + w * kRowsPerWave;
-  const bool active = row0 < a.R;  // wave-uniform: rows past R only help stage
-
-  const int s_cap = a.max_blocks * a.block_size;
-  const int S = min(max(a.seq_lens[b], 0), s_cap);
-  const int ns = a.num_splits;
-  const int chunk = ((S + ns - 1) / ns + (kTile - 1)) & ~(kTile - 1);
-  const int seg_start = min(split * chunk, S);
-  const int seg_end = min(S, seg_start + chunk);
+  // LDS slot swizzle: the 16-byte slot of token t16 (within its 16-token
+  // group) and dims 8q .. 8q + 8 (within the 32-dim k-step) is
+  // 16 q + (t16 ^ 8 (q & 1)). Lane (j, g) therefore copies token j ^ 8 (g & 1)
+  // into slot 16 g + j, and reads its own QK operand (token j) from slot
+  // kslot; the transposing PV reads then hit 32 distinct bank pairs per
+  // half-wave instead of 16.
+  const int js = j ^ ((g & 1) << 3);
+  const int kslot = 16 * g + js;
+  // Waves whose rows all lie past R compute on zero queries (their results are
+  // not stored): a wave-dependent branch around the tile work would make the
+  // compiler copy the accumulators on every tile.
+  const int row0 = rg * kRowsPerGroup + w * kRowsPerWave;
   const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
 
-  // Q^T as the B operand (lane: row j, dims 32 kk + 8 g): k-steps below kQLds
-  // go to this wave's LDS blocks (2w + rb, kk), the rest stay in registers;
-  // and each lane's key limit for its row j.
-  uint4 qf[2][kQRegs];
+  // Q^T as the B operand, all 18 k-steps in registers (lane: row j, dims
+  // 32 kk + 8 g); and each lane's key limit for its row j.
+  uint4 qf[2][kKSteps];
   int lim[2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -126,25 +197,14 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
     const bool live = r < a.R;
     const uint16_t* qrow = a.q + ((size_t)b * a.R + (live ? r : 0)) * kD + 8 * g;
 #pragma unroll
-    for (int kk = 0; kk < kKSteps; ++kk) {
-      const uint4 v = live ? *reinterpret_cast<const uint4*>(qrow + 32 * kk) : make_uint4(0, 0, 0, 0);
-      if (kk < kQLds)
-        *reinterpret_cast<uint4*>(&qlds[((2 * w + rb) * kQLds + kk) * 1024 + 16 * lane]) = v;
-      else
-        qf[rb][kk - kQLds] = v;
-    }
+    for (int kk = 0; kk < kKSteps; ++kk)
+      qf[rb][kk] = live ? *reinterpret_cast<const uint4*>(qrow + 32 * kk) : make_uint4(0, 0, 0, 0);
     const int qi = live ? r / a.h_q : 0;
     lim[rb] = min(seg_end, a.causal ? S - (a.s_q - 1 - qi) : S);
   }
-
-  RowState st[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    st[rb].m = kNegInf;
-    st[rb].lsum = 0.f;
-#pragma unroll
-    for (int nb = 0; nb < kNB; ++nb) st[rb].o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
+  // Let the Q loads land here: a wait left to their first use would sit inside
+  // the tile loop, where it would also wait for every tile copy in flight.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
   const int* bt = a.block_table + (size_t)b * a.max_blocks;
   // The table is read-only for the launch; through the constant address space
@@ -152,159 +212,231 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
   const __attribute__((address_space(4))) int* btc =
       (const __attribute__((address_space(4))) int*)bt;
   const int bs = a.block_size;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const uint32_t tiles_lds = (uint32_t)(uintptr_t)(lds_u8*)&tiles[0][0];
 
-  // Staging: wave w loads blocks w, w + 4, ... of tile k. Tokens at or past
-  // seg_end read the tile's first token instead (masked later), so nothing
-  // outside the request's live cache rows is touched.
-  auto stage_load = [&](int k, uint4 (&r)[kStageLoads]) {
+  // Staging of tile k into ring slot k % kDepth: wave w copies blocks
+  // w + 4 i (i < 9): token group tg = blk / 18, dims 32 kk + 8 g. A lane's
+  // two tokens are 16 tg + j; tokens at or past seg_end read the tile's first
+  // token instead (masked later), so nothing outside the request's live cache
+  // rows is touched. Block ids come from scalar loads, which keeps the vector
+  // memory counter for the copies alone.
+  auto stage = [&](int k) {
     const int ts = seg_start + kTile * k;
+    const uint32_t slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
+    int tok[2];
 #pragma unroll
-    for (int i = 0; i < kStageLoads; ++i) {
-      const int blk = w + kWaves * i;
-      const int tg = blk / kKSteps, kk = blk - tg * kKSteps;
-      const int tl = 16 * tg + j;
-      size_t row;
-      if constexpr (kBlockUniform) {
-        // 32 tokens from a 32-aligned start share one block.
-        const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
-        const int slot0 = ts - (int)lb * bs;
-        row = (size_t)btc[lb] * bs + slot0 + (ts + tl < seg_end ? tl : 0);
-      } else {
-        const int t = ts + tl < seg_end ? ts + tl : ts;
-        const uint32_t lb = gqa::fastdiv((uint32_t)t, a.bs_div);
-        row = (size_t)bt[lb] * bs + (t - (int)lb * bs);
+    for (int tg = 0; tg < 2; ++tg) tok[tg] = ts + 16 * tg + js < seg_end ? 16 * tg + js : 0;
+    if constexpr (kBlockUniform) {
+      // 32 tokens from a 32-aligned start share one block: a uniform base row.
+      const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
+      const size_t row0 = (size_t)btc[lb] * bs + (ts - (int)lb * bs);
+      const uint16_t* base = a.kv + row0 * kD;
+      uint32_t voff[2];
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg) voff[tg] = (uint32_t)(tok[tg] * kD + 8 * g) * 2u;
+#pragma unroll
+      for (int i = 0; i < kStageLoads; ++i) {
+        const int blk = w + kWaves * i;
+        const int tg = blk >= kKSteps ? 1 : 0, kk = blk - tg * kKSteps;
+        load_to_lds(base + 32 * kk, tg ? voff[1] : voff[0],
+                    __builtin_amdgcn_readfirstlane(slot + (uint32_t)blk * 1024));
       }
-      r[i] = gqa::load_kv(a.kv + row * kD + 32 * kk + 8 * g);
+    } else {
+      // The tile's tokens span blocks lb_lo .. lb_hi: fetch their ids with
+      // uniform loads and let each lane take its own.
+      const int t_hi = min(ts + kTile, seg_end) - 1;
+      const int lb_lo = (int)gqa::fastdiv((uint32_t)ts, a.bs_div);
+      const int lb_hi = (int)gqa::fastdiv((uint32_t)t_hi, a.bs_div);
+      int lbl[2];
+      size_t row[2] = {0, 0};
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg) lbl[tg] = (int)gqa::fastdiv((uint32_t)(ts + tok[tg]), a.bs_div);
+      for (int q = lb_lo; q <= lb_hi; ++q) {
+        const size_t id = (size_t)btc[q];
+#pragma unroll
+        for (int tg = 0; tg < 2; ++tg) row[tg] = lbl[tg] == q ? id : row[tg];
+      }
+      const uint16_t* src[2];
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg)
+        src[tg] = a.kv + (row[tg] * bs + (ts + tok[tg] - lbl[tg] * bs)) * kD + 8 * g;
+#pragma unroll
+      for (int i = 0; i < kStageLoads; ++i) {
+        const int blk = w + kWaves * i;
+        const int tg = blk >= kKSteps ? 1 : 0, kk = blk - tg * kKSteps;
+        load_to_lds((tg ? src[1] : src[0]) + 32 * kk,
+                    __builtin_amdgcn_readfirstlane(slot + (uint32_t)blk * 1024));
+      }
     }
   };
-  auto stage_store = [&](int buf, const uint4 (&r)[kStageLoads]) {
-#pragma unroll
-    for (int i = 0; i < kStageLoads; ++i)
-      *reinterpret_cast<uint4*>(&tiles[buf][(w + kWaves * i) * 1024 + 16 * lane]) = r[i];
-  };
 
-  auto consume = [&](int k, int buf) {
-    if (!active) return;
-    const uint8_t* T = tiles[buf];
-    const int ts = seg_start + kTile * k;
-    // QK^T: c[rb][tg][e] = score of token 16 tg + 4 g + e for row j of block rb.
-    f32x4_t c[2][2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int tg = 0; tg < 2; ++tg) c[rb][tg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < kKSteps; ++kk) {
-      uint4 qv[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-        qv[rb] = kk < kQLds ? *reinterpret_cast<const uint4*>(
-                                  &qlds[((2 * w + rb) * kQLds + kk) * 1024 + 16 * lane])
-                            : qf[rb][kk - kQLds];
-#pragma unroll
-      for (int tg = 0; tg < 2; ++tg) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(T + (tg * kKSteps + kk) * 1024 + 16 * lane);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-          c[rb][tg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf), as_bf16x8(qv[rb]),
-                                                              c[rb][tg], 0, 0, 0);
-      }
-      // Keep the operand reads of at most two k-steps ahead of their MFMAs:
-      // hoisting all of them would take more registers than the wave has.
-      if (kk & 1) __builtin_amdgcn_sched_barrier(0);
-    }
+  f32x4_t o[2][kNB];
+  float lsum[2];
+  float mref[2] = {kNegInf, kNegInf};  // row j's reference max (log2 units)
+  float mtrue[2] = {kNegInf, kNegInf};  // row j's max over the split so far
+  bool beaten = false;                  // some row's max beat its reference
 
-    uint32_t pw[2][4];
+  // One pass over the split's tiles, accumulating o and lsum against mref.
+  auto pass = [&]() {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      float s[2][4];
-      float mx = kNegInf;
+      lsum[rb] = 0.f;
 #pragma unroll
-      for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool valid = ts + 16 * tg + 4 * g + e < lim[rb];
-          s[tg][e] = valid ? c[rb][tg][e] * a.scale_log2e : kNegInf;
-          mx = fmaxf(mx, s[tg][e]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(st[rb].m, mx);
-      const float ms = mn == kNegInf ? 0.f : mn;
-      const float alpha = exp2_fast(st[rb].m - ms);
-      st[rb].m = mn;
-      float psum = 0.f;
-#pragma unroll
-      for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          const gqa::bf16x2_t pb = __builtin_convertvector(
-              (float __attribute__((ext_vector_type(2)))){exp2_fast(s[tg][e] - ms),
-                                                          exp2_fast(s[tg][e + 1] - ms)},
-              gqa::bf16x2_t);
-          const uint32_t wd = __builtin_bit_cast(uint32_t, pb);
-          pw[rb][2 * tg + e / 2] = wd;
-          psum += gqa::bf16_lo(wd) + gqa::bf16_hi(wd);
-        }
-      st[rb].lsum = fmaf(st[rb].lsum, alpha, psum);
-      // Rescale O rows (4g + e) when any row's max moved.
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-        float ae[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ae[e] = __shfl(alpha, 4 * g + e, 64);
-#pragma unroll
-        for (int nb = 0; nb < kNB; ++nb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) st[rb].o[nb][e] *= ae[e];
-      }
+      for (int nb = 0; nb < kNB; ++nb) o[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    // Prologue: tiles 0 .. kDepth - 2 in flight; tile 0 published.
+    for (int k = 0; k < kDepth - 1 && k < ntiles; ++k) stage(k);
+    if (ntiles >= kDepth - 1)
+      publish_barrier<kStageLoads * (kDepth - 2)>();
+    else
+      publish_barrier<0>();
+    for (int k = 0; k < ntiles; ++k) {
+      // Refill the slot consumed in the previous iteration (every wave has
+      // passed the barrier that ended it).
+      const bool refill = k + kDepth - 1 < ntiles;
+      if (refill) stage(k + kDepth - 1);
+      const uint8_t* T = tiles[k % kDepth];
+      const int ts = seg_start + kTile * k;
 
-    // PV. Lane (j, g) supplies token 4g + j/4 (and 16 more), dims
-    // 16nb + 4(j%4) .. +4 of the A-order tile.
-    const int rr = 4 * g + (j >> 2);
+      // QK^T: c[rb][tg][e] = score of token 16 tg + 4 g + e for row j of block rb.
+      // Operand reads run kQKAhead k-steps ahead of their MFMAs (the
+      // scheduling barriers keep the compiler from sinking them to their use).
+      auto read_k = [&](int kk, int tg) -> uint4 {
+        return *reinterpret_cast<const uint4*>(T + (tg * kKSteps + kk) * 1024 + 16 * kslot);
+      };
+      f32x4_t c[2][2];
 #pragma unroll
-    for (int nb = 0; nb < kNB; ++nb) {
-      const int kk = nb >> 1;
-      const int gg = 2 * (nb & 1) + ((j & 3) >> 1);
-      const uint32_t off = (uint32_t)kk * 1024 + 16u * (uint32_t)(rr + 16 * gg) + 8u * (j & 1);
-      const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off));
-      const bf16x4_t v1 =
-          __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off + kKSteps * 1024));
-      const bf16x8_t vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int tg = 0; tg < 2; ++tg) c[rb][tg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      uint4 kr[kQKAhead + 1][2];
+#pragma unroll
+      for (int kk = 0; kk < kQKAhead; ++kk)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) kr[kk][x] = read_k(kk, x);
+#pragma unroll
+      for (int kk = 0; kk < kKSteps; ++kk) {
+        if (kk + kQKAhead < kKSteps) {
+          const int sl = (kk + kQKAhead) % (kQKAhead + 1);
+#pragma unroll
+          for (int x = 0; x < 2; ++x) kr[sl][x] = read_k(kk + kQKAhead, x);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int sl = kk % (kQKAhead + 1);
+#pragma unroll
+        for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+            c[rb][tg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                as_bf16x8(kr[sl][tg]), as_bf16x8(qf[rb][kk]), c[rb][tg], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+
+      // V operands for PV, read kPVAhead column blocks ahead of their MFMAs;
+      // the first ones are issued before the softmax. Lane (j, g) supplies
+      // token 4g + j/4 (and 16 more), dims 16nb + 4(j%4) .. +4 of the A-order
+      // tile; the transposing read hands lane x the four tokens of dim 16nb + x.
+      const int rr = 4 * g + (j >> 2);
+      auto read_v = [&](int nb) -> bf16x8_t {
+        const int kk = nb >> 1;
+        const int gg = 2 * (nb & 1) + ((j & 3) >> 1);
+        const uint32_t off =
+            (uint32_t)kk * 1024 + 16u * (uint32_t)(16 * gg + (rr ^ ((gg & 1) << 3))) + 8u * (j & 1);
+        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off));
+        const bf16x4_t v1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off + kKSteps * 1024));
+        return bf16x8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      };
+      bf16x8_t vr[kPVAhead + 1];
+#pragma unroll
+      for (int nb = 0; nb < kPVAhead; ++nb) vr[nb] = read_v(nb);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // Probabilities against the reference max, rounded to bf16 (l sums the
+      // rounded values).
+      uint32_t pw[2][4];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const bf16x8_t pa =
-            as_bf16x8(make_uint4(pw[rb][0], pw[rb][1], pw[rb][2], pw[rb][3]));
-        st[rb].o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, st[rb].o[nb], 0, 0, 0);
+        float sc[2][4];
+        float mx = kNegInf;
+#pragma unroll
+        for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool valid = ts + 16 * tg + 4 * g + e < lim[rb];
+            sc[tg][e] = valid ? c[rb][tg][e] * a.scale_log2e : kNegInf;
+            mx = fmaxf(mx, sc[tg][e]);
+          }
+        // mx is this lane's max (its 8 tokens of row j). The row's first live
+        // tile sets the reference (nothing is accumulated before it, so
+        // nothing needs rescaling); the row's four lanes agree on it.
+        mref[rb] = mref[rb] == kNegInf ? row_max(mx) : mref[rb];
+        beaten |= mx > mref[rb] + kRefSlack;
+        mtrue[rb] = fmaxf(mtrue[rb], mx);  // lane-local until a second pass
+        const float base = mref[rb] == kNegInf ? 0.f : mref[rb];
+        float psum = 0.f;
+#pragma unroll
+        for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            const gqa::bf16x2_t pb = __builtin_convertvector(
+                (float __attribute__((ext_vector_type(2)))){exp2_fast(sc[tg][e] - base),
+                                                            exp2_fast(sc[tg][e + 1] - base)},
+                gqa::bf16x2_t);
+            const uint32_t wd = __builtin_bit_cast(uint32_t, pb);
+            pw[rb][2 * tg + e / 2] = wd;
+            psum += gqa::bf16_lo(wd) + gqa::bf16_hi(wd);
+          }
+        lsum[rb] += psum;
       }
-      if (nb & 1) __builtin_amdgcn_sched_barrier(0);
+
+      // PV: o[rb][nb] += P[16 rows x 32 tok] . V[32 tok x dims 16nb .. +16].
+#pragma unroll
+      for (int nb = 0; nb < kNB; ++nb) {
+        if (nb + kPVAhead < kNB) vr[(nb + kPVAhead) % (kPVAhead + 1)] = read_v(nb + kPVAhead);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const bf16x8_t pa =
+              as_bf16x8(make_uint4(pw[rb][0], pw[rb][1], pw[rb][2], pw[rb][3]));
+          o[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vr[nb % (kPVAhead + 1)],
+                                                              o[rb][nb], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Tile k + 1 must have landed; the later ones stay in flight.
+      if (refill)
+        publish_barrier<kStageLoads * (kDepth - 2)>();
+      else
+        publish_barrier<0>();
     }
   };
 
-  if (ntiles > 0) {
-    uint4 r[kStageLoads];
-    stage_load(0, r);
-    stage_store(0, r);
-    __syncthreads();
-    for (int k = 0; k < ntiles; ++k) {
-      const int buf = k & 1;
-      if (k + 1 < ntiles) stage_load(k + 1, r);
-      consume(k, buf);
-      if (k + 1 < ntiles) stage_store(buf ^ 1, r);
-      __syncthreads();
+  pass();
+  // A row whose max beat its reference by more than kRefSlack has overflowed
+  // or lost precision: the workgroup (which stages tiles together) runs the
+  // split again with every row's reference at its true max (probabilities
+  // <= 1, so a second pass always suffices).
+  if (lane == 0) restart_vote[w] = __builtin_amdgcn_ballot_w64(beaten) != 0;
+  __syncthreads();
+  if (restart_vote[0] | restart_vote[1] | restart_vote[2] | restart_vote[3]) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      mref[rb] = row_max(mtrue[rb]);
     }
+    pass();
   }
-  if (!active) return;
 
   // Final (m, l) of the rows this lane's o entries hold: rows 4g + e.
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    float L = st[rb].lsum + __shfl_xor(st[rb].lsum, 16, 64);
+    float L = lsum[rb] + __shfl_xor(lsum[rb], 16, 64);
     L += __shfl_xor(L, 32, 64);
     float Me[4], Le[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      Me[e] = __shfl(st[rb].m, 4 * g + e, 64);
+      Me[e] = __shfl(mref[rb], 4 * g + e, 64);
       Le[e] = __shfl(L, 4 * g + e, 64);
     }
 #pragma unroll
@@ -312,22 +444,22 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
       const int row = row0 + 16 * rb + 4 * g + e;
       if (row >= a.R) continue;
       const size_t br = (size_t)b * a.R + row;
-      if (ns == 1) {
+      if (po.direct) {
         const float inv = Le[e] > 0.f ? 1.f / Le[e] : 0.f;
 #pragma unroll
         for (int nb = 0; nb < kNB; ++nb)
-          a.out[br * kDV + 16 * nb + j] = (uint16_t)f32_to_bf16_bits(st[rb].o[nb][e] * inv);
+          a.out[br * kDV + 16 * nb + j] = (uint16_t)f32_to_bf16_bits(o[rb][nb][e] * inv);
         if (a.lse && j == 0) {
           const int qi = row / a.h_q, h = row - qi * a.h_q;
           a.lse[((size_t)b * a.h_q + h) * a.s_q + qi] =
               Le[e] > 0.f ? Me[e] * kLn2 + logf(Le[e]) : kNegInf;
         }
       } else {
-        const size_t sx = br * ns + split;
+        const size_t sx = po.st_base + (size_t)row * po.st_stride;
 #pragma unroll
-        for (int nb = 0; nb < kNB; ++nb) a.ws_acc[sx * kDV + 16 * nb + j] = st[rb].o[nb][e];
+        for (int nb = 0; nb < kNB; ++nb) a.ws_acc[sx * kDV + 16 * nb + j] = o[rb][nb][e];
         if (j == 0) {
-          a.ws_m[sx] = Me[e] == kNegInf ? kNegInf : Me[e] * kLn2;  // natural-log units
+          a.ws_m[sx] = Le[e] > 0.f ? Me[e] * kLn2 : kNegInf;  // natural-log units
           a.ws_l[sx] = Le[e];
         }
       }
@@ -335,28 +467,46 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
   }
 }
 
-// Log-sum-exp merge of the splits of each (request, query row) in split order:
-// one wave per row, lane i owns dims 8i .. 8i + 8.
-__global__ __launch_bounds__(256) void mla_decode_merge_kernel(const MlaArgs a) {
+// Fixed splits: workgroup (rg, b, split) takes split `split` of request b,
+// cut at multiples of 32 tokens.
+template <bool kBlockUniform>
+__global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t tiles[kDepth][kTileBytes];
+  __shared__ int restart_vote[kWaves];
+  const int b = blockIdx.y, split = blockIdx.z;
+  const int s_cap = a.max_blocks * a.block_size;
+  const int S = min(max(a.seq_lens[b], 0), s_cap);
+  const int ns = a.num_splits;
+  const int chunk = ((S + ns - 1) / ns + (kTile - 1)) & ~(kTile - 1);
+  const int seg_start = min(split * chunk, S);
+  const int seg_end = min(S, seg_start + chunk);
+  PieceOut po;
+  po.direct = ns == 1;
+  po.st_base = (size_t)b * a.R * ns + split;
+  po.st_stride = ns;
+  mla_piece<kBlockUniform>(a, tiles, restart_vote, b, blockIdx.x, S, seg_start, seg_end, po);
+}
+
+// Log-sum-exp fold of `count` states of one (request, query row), in order,
+// into out and lse: one wave per row, lane i owns dims 8i .. 8i + 8. index(i)
+// is the state index of the i-th; states with m = -inf (no key) add nothing.
+template <typename IndexFn>
+__device__ __forceinline__ void merge_row(const MlaArgs& a, size_t br, int count, IndexFn index) {
   constexpr int kBatch = 8;
   const int lane = threadIdx.x & 63;
-  const size_t br = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (br >= (size_t)a.B * a.R) return;
-  const int ns = a.num_splits;
-  const size_t st0 = br * ns;
   float mloc = kNegInf;
-  for (int i = lane; i < ns; i += 64) mloc = fmaxf(mloc, a.ws_m[st0 + i]);
+  for (int i = lane; i < count; i += 64) mloc = fmaxf(mloc, a.ws_m[index(i)]);
   const float M = gqa::wave_max(mloc);
   float L = 0.f, A[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) A[d] = 0.f;
   if (M != kNegInf) {
-    for (int i0 = 0; i0 < ns; i0 += kBatch) {
+    for (int i0 = 0; i0 < count; i0 += kBatch) {
       float mi[kBatch], li[kBatch];
       float4 a0[kBatch], a1[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
-        const size_t sx = st0 + min(i0 + k, ns - 1);  // past the end: a valid split, not folded
+        const size_t sx = index(min(i0 + k, count - 1));  // past the end: valid, not folded
         mi[k] = a.ws_m[sx];
         li[k] = a.ws_l[sx];
         const float4* src = reinterpret_cast<const float4*>(a.ws_acc + sx * kDV + 8 * lane);
@@ -365,8 +515,8 @@ __global__ __launch_bounds__(256) void mla_decode_merge_kernel(const MlaArgs a) 
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
-        if (i0 + k >= ns) break;
-        // Exactly 1 for the split holding the max; 0 for empty splits.
+        if (i0 + k >= count) break;
+        // Exactly 1 for the state holding the max; 0 for empty states.
         const float f = mi[k] == M ? 1.f : exp2_fast((mi[k] - M) * kLog2e);
         const float av[8] = {a0[k].x, a0[k].y, a0[k].z, a0[k].w, a1[k].x, a1[k].y, a1[k].z, a1[k].w};
         L = fmaf(li[k], f, L);
@@ -386,6 +536,136 @@ __global__ __launch_bounds__(256) void mla_decode_merge_kernel(const MlaArgs a) 
     const int qi = row / a.h_q, h = row - qi * a.h_q;
     a.lse[((size_t)b * a.h_q + h) * a.s_q + qi] = L > 0.f ? M + logf(L) : kNegInf;
   }
+}
+
+// Fixed splits: the num_splits states of each row, in split order.
+__global__ __launch_bounds__(256) void mla_decode_merge_kernel(const MlaArgs a) {
+  const size_t br = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (br >= (size_t)a.B * a.R) return;
+  const int ns = a.num_splits;
+  merge_row(a, br, ns, [&](int i) { return br * ns + i; });
+}
+
+// ---------------------------------------------------------------------------
+// Token-balanced launch. The work is the concatenation, in request order, of
+// every request's 32-token tiles: T = sum_b ceil(S_b / 32). Share w of
+// nshare (one workgroup per row group) takes tiles [w T / n, (w + 1) T / n)
+// -- equal to within one tile, whatever the lengths -- and walks them piece
+// by piece (a piece: the share's tiles of one request). A piece that is a
+// whole request is normalised into out directly; only a share's first and
+// last piece can be partial, and their states go to the share's two slots
+// (2w, 2w + 1). The merge then folds each cut request's pieces in share order,
+// so results are bitwise reproducible for a given nshare. With fewer tiles
+// than shares, only the first T shares take work (one tile each), so every
+// working share is non-empty.
+
+// Share w's first tile.
+__device__ __forceinline__ uint64_t share_start(uint64_t T, int w, int n) {
+  return (uint64_t)w * T / (uint64_t)n;
+}
+
+// Tile prefix sums pre[b] = sum_{b' < b} ceil(S_b' / 32) (b = 0..B, S clamped
+// to the block table), the working share count pre[B + 1] = min(nshare, T),
+// and each working share's first request (the first b with pre[b + 1] > its
+// first tile); one workgroup.
+__global__ __launch_bounds__(256) void mla_plan_kernel(const MlaArgs a, uint64_t* pre, int* first) {
+  __shared__ uint64_t part[256];
+  const int tid = threadIdx.x;
+  const int per = (a.B + 255) / 256;
+  const int b0 = min(tid * per, a.B), b1 = min(b0 + per, a.B);
+  const int s_cap = a.max_blocks * a.block_size;
+  auto tiles_of = [&](int b) -> uint64_t {
+    const int S = min(max(a.seq_lens[b], 0), s_cap);
+    return (uint64_t)((S + kTile - 1) / kTile);
+  };
+  uint64_t sum = 0;
+  for (int b = b0; b < b1; ++b) sum += tiles_of(b);
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan of the 256 partial sums
+    const uint64_t v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  uint64_t run = part[tid] - sum;
+  for (int b = b0; b < b1; ++b) {
+    pre[b] = run;
+    run += tiles_of(b);
+  }
+  const uint64_t T = part[255];
+  const int n = (int)(T < (uint64_t)a.nshare ? T : (uint64_t)a.nshare);
+  if (tid == 0) {
+    pre[a.B] = T;
+    pre[a.B + 1] = (uint64_t)n;
+  }
+  __syncthreads();  // the prefix sums, written by all threads, are read below
+  for (int w = tid; w < n; w += 256) {
+    const uint64_t t = share_start(T, w, n);
+    int lo = 0, hi = a.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pre[mid + 1] > t) hi = mid; else lo = mid + 1;
+    }
+    first[w] = lo;
+  }
+}
+
+// Workgroup (w, rg): share w of row group rg.
+template <bool kBlockUniform>
+__global__ __launch_bounds__(256, 1) void mla_decode_balanced_kernel(const MlaArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t tiles[kDepth][kTileBytes];
+  __shared__ int restart_vote[kWaves];
+  const int w = blockIdx.x, rg = blockIdx.y;
+  const int s_cap = a.max_blocks * a.block_size;
+  const uint64_t T = a.pre[a.B];
+  const int n = (int)a.pre[a.B + 1];
+  if (w >= n) return;
+  const uint64_t t0 = share_start(T, w, n), t_end = share_start(T, w + 1, n);
+  int b = a.first[w];
+  for (uint64_t t = t0; t < t_end; ++b) {
+    const uint64_t p0 = a.pre[b], p1 = a.pre[b + 1];
+    if (p1 <= t) continue;  // a request with no tiles
+    const uint64_t t1 = p1 < t_end ? p1 : t_end;
+    const int S = min(max(a.seq_lens[b], 0), s_cap);
+    PieceOut po;
+    po.direct = t == p0 && t1 == p1;
+    po.st_base = (size_t)(2 * w + (t == t0 ? 0 : 1)) * a.R;
+    po.st_stride = 1;
+    mla_piece<kBlockUniform>(a, tiles, restart_vote, b, rg, S, (int)(t - p0) * kTile,
+                             min(S, (int)(t1 - p0) * kTile), po);
+    t = t1;
+  }
+}
+
+// Rows of requests cut by share boundaries: fold their pieces in share order
+// (shares with no tiles hold no piece). Requests with no tiles get out = 0 and
+// lse = -inf; whole pieces were written by the decode kernel.
+__global__ __launch_bounds__(256) void mla_decode_balanced_merge_kernel(const MlaArgs a) {
+  const size_t br = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (br >= (size_t)a.B * a.R) return;
+  const int b = (int)(br / a.R), row = (int)(br - (size_t)b * a.R);
+  const uint64_t p0 = a.pre[b], p1 = a.pre[b + 1], T = a.pre[a.B];
+  const int n = (int)a.pre[a.B + 1];
+  if (p1 == p0) {
+    const int lane = threadIdx.x & 63;
+    *reinterpret_cast<uint4*>(a.out + br * kDV + 8 * lane) = make_uint4(0, 0, 0, 0);
+    if (a.lse && lane == 0) {
+      const int qi = row / a.h_q, h = row - qi * a.h_q;
+      a.lse[((size_t)b * a.h_q + h) * a.s_q + qi] = kNegInf;
+    }
+    return;
+  }
+  // Shares holding tile p0 and tile p1 - 1: the largest w with start(w) <= t.
+  const int w_lo = (int)(((p0 + 1) * (uint64_t)n - 1) / T);
+  const int w_hi = (int)((p1 * (uint64_t)n - 1) / T);
+  if (w_lo == w_hi) return;
+  // Pieces: share w_lo's last slot (its first if the request starts the
+  // share), then the first slot of each later share up to w_hi.
+  const int first_slot = 2 * w_lo + (p0 > share_start(T, w_lo, n) ? 1 : 0);
+  merge_row(a, br, w_hi - w_lo + 1, [&](int i) {
+    return (size_t)(i == 0 ? first_slot : 2 * (w_lo + i)) * a.R + row;
+  });
 }
 
 }  // namespace mla
@@ -409,55 +689,178 @@ extern "C" int mla_decode_pick_num_splits(int B, int s_q, int h_q, int block_siz
   return (int)std::max<int64_t>(ns, 1);
 }
 
-extern "C" int mla_decode_launch(const uint16_t* q, const uint16_t* kv_cache, const int* block_table,
-                                 const int* seq_lens, uint16_t* out, float* lse, int B, int s_q,
-                                 int h_q, int block_size, int max_blocks, float scale, int causal,
-                                 int num_splits, void* workspace, size_t workspace_bytes,
-                                 hipStream_t stream) {
+namespace {
+
+// Checks the launch arguments and fills the kernel arguments; hipSuccess or
+// hipErrorInvalidValue. A zero-request batch returns hipSuccess with a->B 0.
+hipError_t make_args(mla::MlaArgs* a, const uint16_t* q, const uint16_t* kv_cache,
+                     const int* block_table, const int* seq_lens, uint16_t* out, float* lse,
+                     int B, int s_q, int h_q, int block_size, int max_blocks, float scale,
+                     int causal, int num_splits, void* workspace, size_t workspace_bytes) {
   if (B < 0 || B > 65535 || s_q < 1 || h_q < 1 || block_size < 1 || max_blocks < 1)
     return hipErrorInvalidValue;
   const int64_t R = (int64_t)s_q * h_q;
   if (R > (int64_t(1) << 20) || (int64_t)B * R > (int64_t(1) << 31)) return hipErrorInvalidValue;
   if ((int64_t)block_size * max_blocks >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   if (num_splits < 1 || num_splits > MLA_DECODE_MAX_SPLITS) return hipErrorInvalidValue;
+  a->B = B;
   if (B == 0) return hipSuccess;
   if (!q || !kv_cache || !block_table || !seq_lens || !out) return hipErrorInvalidValue;
-  mla::MlaArgs a;
-  a.q = q;
-  a.kv = kv_cache;
-  a.block_table = block_table;
-  a.seq_lens = seq_lens;
-  a.out = out;
-  a.lse = lse;
-  a.ws_acc = a.ws_m = a.ws_l = nullptr;
-  a.B = B;
-  a.s_q = s_q;
-  a.h_q = h_q;
-  a.R = (int)R;
-  a.block_size = block_size;
-  a.max_blocks = max_blocks;
-  a.num_splits = num_splits;
-  a.causal = causal ? 1 : 0;
-  a.bs_div = gqa::make_fastdiv((uint32_t)block_size);
-  a.scale_log2e = (float)((double)scale * 1.4426950408889634);
+  a->q = q;
+  a->kv = kv_cache;
+  a->block_table = block_table;
+  a->seq_lens = seq_lens;
+  a->out = out;
+  a->lse = lse;
+  a->ws_acc = a->ws_m = a->ws_l = nullptr;
+  a->pre = nullptr;
+  a->first = nullptr;
+  a->nshare = 0;
+  a->s_q = s_q;
+  a->h_q = h_q;
+  a->R = (int)R;
+  a->block_size = block_size;
+  a->max_blocks = max_blocks;
+  a->num_splits = num_splits;
+  a->causal = causal ? 1 : 0;
+  a->bs_div = gqa::make_fastdiv((uint32_t)block_size);
+  a->scale_log2e = (float)((double)scale * 1.4426950408889634);
   if (num_splits > 1) {
     if (!workspace || ((uintptr_t)workspace & 15) != 0 ||
         workspace_bytes < mla_decode_workspace_bytes(B, s_q, h_q, num_splits))
       return hipErrorInvalidValue;
     const size_t states = (size_t)B * R * num_splits;
-    a.ws_acc = static_cast<float*>(workspace);
-    a.ws_m = a.ws_acc + states * mla::kDV;
-    a.ws_l = a.ws_m + states;
+    a->ws_acc = static_cast<float*>(workspace);
+    a->ws_m = a->ws_acc + states * mla::kDV;
+    a->ws_l = a->ws_m + states;
   }
-  const dim3 grid((unsigned)((R + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup), B, num_splits);
-  if (block_size % mla::kTile == 0)
+  return hipSuccess;
+}
+
+hipError_t launch_splitkv(const mla::MlaArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.R + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup), a.B,
+                  a.num_splits);
+  if (a.block_size % mla::kTile == 0)
     hipLaunchKernelGGL(mla::mla_decode_kernel<true>, grid, dim3(256), 0, stream, a);
   else
     hipLaunchKernelGGL(mla::mla_decode_kernel<false>, grid, dim3(256), 0, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || num_splits == 1) return err;
-  const size_t rows = (size_t)B * R;
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const mla::MlaArgs& a, hipStream_t stream) {
+  const size_t rows = (size_t)a.B * a.R;
   hipLaunchKernelGGL(mla::mla_decode_merge_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                      stream, a);
   return hipGetLastError();
 }
+
+}  // namespace
+
+extern "C" int mla_decode_launch(const uint16_t* q, const uint16_t* kv_cache, const int* block_table,
+                                 const int* seq_lens, uint16_t* out, float* lse, int B, int s_q,
+                                 int h_q, int block_size, int max_blocks, float scale, int causal,
+                                 int num_splits, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+  mla::MlaArgs a;
+  hipError_t err = make_args(&a, q, kv_cache, block_table, seq_lens, out, lse, B, s_q, h_q,
+                             block_size, max_blocks, scale, causal, num_splits, workspace,
+                             workspace_bytes);
+  if (err != hipSuccess || a.B == 0) return err;
+  err = launch_splitkv(a, stream);
+  if (err != hipSuccess || num_splits == 1) return err;
+  return launch_combine(a, stream);
+}
+
+extern "C" int mla_decode_splitkv_launch(const uint16_t* q, const uint16_t* kv_cache,
+                                         const int* block_table, const int* seq_lens,
+                                         uint16_t* out, float* lse, int B, int s_q, int h_q,
+                                         int block_size, int max_blocks, float scale, int causal,
+                                         int num_splits, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+  mla::MlaArgs a;
+  hipError_t err = make_args(&a, q, kv_cache, block_table, seq_lens, out, lse, B, s_q, h_q,
+                             block_size, max_blocks, scale, causal, num_splits, workspace,
+                             workspace_bytes);
+  if (err != hipSuccess || a.B == 0) return err;
+  return launch_splitkv(a, stream);
+}
+
+extern "C" int mla_decode_combine_launch(void* workspace, size_t workspace_bytes, uint16_t* out,
+                                         float* lse, int B, int s_q, int h_q, int num_splits,
+                                         hipStream_t stream) {
+  if (num_splits < 2) return hipErrorInvalidValue;
+  // The combine kernel reads only the workspace and writes out and lse; the
+  // other arguments only size the grid, so placeholders stand in for the
+  // split kernel's inputs.
+  static const uint16_t kNone = 0;
+  static const int kNoInt = 0;
+  mla::MlaArgs a;
+  hipError_t err = make_args(&a, &kNone, &kNone, &kNoInt, &kNoInt, out, lse, B, s_q, h_q, 1, 1,
+                             1.f, 0, num_splits, workspace, workspace_bytes);
+  if (err != hipSuccess || a.B == 0) return err;
+  return launch_combine(a, stream);
+}
+
+namespace {
+
+constexpr int kMaxShares = 8192;
+
+// Shares per row group of a balanced launch: num_workgroups (<= 0: the
+// device's CU count) spread over the ceil(R / 128) row groups.
+int balanced_shares(int s_q, int h_q, int num_workgroups) {
+  if (num_workgroups <= 0 && (num_workgroups = gqa::device_cu_count()) <= 0) return 0;
+  const int64_t rg = ((int64_t)s_q * h_q + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup;
+  return (int)std::min<int64_t>(kMaxShares, std::max<int64_t>(1, num_workgroups / rg));
+}
+
+size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
+
+}  // namespace
+
+extern "C" size_t mla_decode_balanced_workspace_bytes(int B, int s_q, int h_q, int num_workgroups) {
+  if (B <= 0 || s_q <= 0 || h_q <= 0) return 0;
+  const int n = balanced_shares(s_q, h_q, num_workgroups);
+  if (n <= 0) return 0;
+  const size_t states = (size_t)2 * n * s_q * h_q;
+  return align16(states * (mla::kDV + 2) * sizeof(float)) + align16((size_t)(B + 2) * 8) +
+         (size_t)n * sizeof(int);
+}
+
+extern "C" int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_cache,
+                                          const int* block_table, const int* seq_lens,
+                                          uint16_t* out, float* lse, int B, int s_q, int h_q,
+                                          int block_size, int max_blocks, float scale, int causal,
+                                          int num_workgroups, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+  mla::MlaArgs a;
+  hipError_t err = make_args(&a, q, kv_cache, block_table, seq_lens, out, lse, B, s_q, h_q,
+                             block_size, max_blocks, scale, causal, 1, nullptr, 0);
+  if (err != hipSuccess || a.B == 0) return err;
+  const int n = balanced_shares(s_q, h_q, num_workgroups);
+  const size_t need = mla_decode_balanced_workspace_bytes(B, s_q, h_q, num_workgroups);
+  if (n <= 0 || !workspace || ((uintptr_t)workspace & 15) != 0 || workspace_bytes < need)
+    return hipErrorInvalidValue;
+  const size_t states = (size_t)2 * n * a.R;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  a.ws_acc = reinterpret_cast<float*>(ws);
+  a.ws_m = a.ws_acc + states * mla::kDV;
+  a.ws_l = a.ws_m + states;
+  uint64_t* pre = reinterpret_cast<uint64_t*>(ws + align16(states * (mla::kDV + 2) * sizeof(float)));
+  int* first = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(pre) + align16((size_t)(B + 2) * 8));
+  a.pre = pre;
+  a.first = first;
+  a.nshare = n;
+  hipLaunchKernelGGL(mla::mla_plan_kernel, dim3(1), dim3(256), 0, stream, a, pre, first);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  const unsigned rg = (unsigned)((a.R + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup);
+  if (block_size % mla::kTile == 0)
+    hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<true>, dim3(n, rg), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<false>, dim3(n, rg), dim3(256), 0, stream, a);
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  const size_t rows = (size_t)B * a.R;
+  hipLaunchKernelGGL(mla::mla_decode_balanced_merge_kernel, dim3((unsigned)((rows + 3) / 4)),
+                     dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+

@@ -77,9 +77,15 @@ def lib():
             fn.restype = _i
         L.gqa_decode_prefer_balanced.argtypes = [_i, _i, _i, _i, _i, _i]
         L.gqa_decode_prefer_balanced.restype = _i
-        L.mla_decode_launch.argtypes = [_vp] * 6 + [_i] * 5 + [ctypes.c_float, _i, _i, _vp,
-                                                                ctypes.c_size_t, _vp]
-        L.mla_decode_launch.restype = _i
+        for fn in (L.mla_decode_launch, L.mla_decode_splitkv_launch, L.mla_decode_balanced_launch):
+            fn.argtypes = [_vp] * 6 + [_i] * 5 + [ctypes.c_float, _i, _i, _vp, ctypes.c_size_t,
+                                                  _vp]
+            fn.restype = _i
+        L.mla_decode_combine_launch.argtypes = [_vp, ctypes.c_size_t, _vp, _vp, _i, _i, _i, _i,
+                                                _vp]
+        L.mla_decode_combine_launch.restype = _i
+        L.mla_decode_balanced_workspace_bytes.argtypes = [_i] * 4
+        L.mla_decode_balanced_workspace_bytes.restype = ctypes.c_size_t
         L.mla_decode_workspace_bytes.argtypes = [_i] * 4
         L.mla_decode_workspace_bytes.restype = ctypes.c_size_t
         L.mla_decode_pick_num_splits.argtypes = [_i] * 6
@@ -150,6 +156,22 @@ def prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus):
 
 def mla_launch(*args):
     return lib().mla_decode_launch(*args)
+
+
+def mla_splitkv_launch(*args):
+    return lib().mla_decode_splitkv_launch(*args)
+
+
+def mla_combine_launch(*args):
+    return lib().mla_decode_combine_launch(*args)
+
+
+def mla_balanced_launch(*args):
+    return lib().mla_decode_balanced_launch(*args)
+
+
+def mla_balanced_workspace_bytes(B, s_q, h_q, num_workgroups):
+    return lib().mla_decode_balanced_workspace_bytes(B, s_q, h_q, num_workgroups)
 
 
 def mla_workspace_bytes(B, s_q, h_q, num_splits):

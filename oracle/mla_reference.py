@@ -75,15 +75,3 @@ def mla_decode_ref(q, kv_cache, block_table, seq_lens, scale, causal=False, dv=D
             out[i, qi] = (p / l) @ C[:lim, :dv]
             lse[i, :, qi] = (m + np.log(l))[:, 0]
     return out.astype(np.float32), lse.astype(np.float32)
-
-
-def mla_flops_bytes(seq_lens, s_q, h_q, dv=DV):
-    """FlashMLA's accounting of one decode step (FLOPs of QK and PV over every
-    query row and key; bytes of q, the latent rows once and the output), the
-    numbers its benchmark divides by the time. The key count per request is
-    its length (no causal discount), as FlashMLA counts."""
-    total = float(np.sum(np.maximum(np.asarray(seq_lens, dtype=np.float64), 0)))
-    B = len(seq_lens)
-    flops = 2.0 * s_q * h_q * total * (D + dv)
-    nbytes = B * s_q * h_q * D * 2 + total * D * 2 + B * s_q * h_q * dv * 2
-    return flops, nbytes

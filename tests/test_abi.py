@@ -391,7 +391,9 @@ def test_op_check_order_and_messages(binding):
 
 def test_mla_exports():
     declared = capi.declared_mla_functions()
-    assert declared == ["mla_decode_launch", "mla_decode_pick_num_splits",
+    assert declared == ["mla_decode_balanced_launch", "mla_decode_balanced_workspace_bytes",
+                        "mla_decode_combine_launch", "mla_decode_launch",
+                        "mla_decode_pick_num_splits", "mla_decode_splitkv_launch",
                         "mla_decode_workspace_bytes"]
     import subprocess
 
@@ -405,6 +407,18 @@ def test_mla_exports():
 def test_mla_workspace_bytes(B, s_q, h_q, ns):
     assert capi.mla_workspace_bytes(B, s_q, h_q, ns) == B * s_q * h_q * ns * (512 + 2) * 4
     assert capi.mla_workspace_bytes(B, s_q, h_q, 1) == 0
+
+
+@pytest.mark.parametrize("B,s_q,h_q,nwg", [(128, 1, 128, 256), (1, 2, 128, 256), (7, 1, 16, 100),
+                                           (3, 2, 200, 64)])
+def test_mla_balanced_workspace_bytes(B, s_q, h_q, nwg):
+    R = s_q * h_q
+    n = max(1, nwg // ((R + 127) // 128))
+    states = 2 * n * R
+    a16 = lambda x: (x + 15) // 16 * 16  # noqa: E731
+    want = a16(states * 514 * 4) + a16((B + 2) * 8) + n * 4
+    assert capi.mla_balanced_workspace_bytes(B, s_q, h_q, nwg) == want
+    assert capi.mla_balanced_workspace_bytes(0, s_q, h_q, nwg) == 0
 
 
 def test_mla_pick_num_splits():
@@ -433,8 +447,31 @@ def mla_args(**over):
                                                                              ws=FAKE)])
 def test_mla_rejects_bad_arguments(over):
     assert capi.mla_launch(*mla_args(**over)) == INVALID
+    assert capi.mla_splitkv_launch(*mla_args(**over)) == INVALID
+
+
+@pytest.mark.parametrize("over", [dict(B=-1), dict(B=70000), dict(s_q=0), dict(h_q=0),
+                                  dict(bs=0), dict(mb=0), dict(q=None), dict(kv=None),
+                                  dict(bt=None), dict(sl=None), dict(out=None), dict(ws=None),
+                                  dict(ws=FAKE + 4), dict(wsb=16)])
+def test_mla_balanced_rejects_bad_arguments(over):
+    a = mla_args(**{**dict(ns=256, ws=FAKE, wsb=1 << 30), **over})
+    assert capi.mla_balanced_launch(*a) == INVALID
+
+
+@pytest.mark.parametrize("over", [dict(ns=1), dict(ns=0), dict(ns=129), dict(B=-1),
+                                  dict(s_q=0), dict(h_q=0), dict(out=None), dict(ws=None),
+                                  dict(ws=FAKE + 4), dict(wsb=16)])
+def test_mla_combine_rejects_bad_arguments(over):
+    a = dict(ws=FAKE, wsb=1 << 30, out=FAKE, lse=FAKE, B=2, s_q=1, h_q=16, ns=4)
+    a.update(over)
+    assert capi.mla_combine_launch(*[a[k] for k in ("ws", "wsb", "out", "lse", "B", "s_q", "h_q",
+                                                    "ns")], None) == INVALID
 
 
 def test_mla_empty_batch_is_a_no_op():
     assert capi.mla_launch(*mla_args(B=0, q=None, kv=None, bt=None, sl=None, out=None,
                                      lse=None)) == capi.HIP_SUCCESS
+    assert capi.mla_combine_launch(None, 0, None, None, 0, 1, 16, 4, None) == capi.HIP_SUCCESS
+    assert capi.mla_balanced_launch(*mla_args(B=0, q=None, kv=None, bt=None, sl=None, out=None,
+                                              lse=None, ns=256)) == capi.HIP_SUCCESS

@@ -155,3 +155,138 @@ def test_benchmark_batch(gpu):
     ns = capi.mla_pick_num_splits(cfg["B"], 1, 128, 64, case[2].shape[1], 0)
     rows = [0, 17, 40, 63, 64, 99, 120, 127]
     check(run(case, False, ns), oracle(case, False, rows), "mla_4k", rows=rows)
+
+
+@pytest.mark.parametrize("ns", [1, 2, 5])
+def test_split_and_combine_launches(gpu, ns):
+    # The two halves of mla_decode_launch, launched apart, give its bits.
+    case = mla_case(mla_seq_lens(5, 900, seed=5, s_q=2), 2, 64, seed=5)
+    q, kv, bt, sl = case
+    B, s_q, h_q, _ = q.shape
+    want = run(case, True, ns)
+    out = torch.empty_like(want[0])
+    lse = torch.empty_like(want[1])
+    wsb = capi.mla_workspace_bytes(B, s_q, h_q, ns)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
+    sp = torch.cuda.current_stream().cuda_stream
+    assert capi.mla_splitkv_launch(q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                   out.data_ptr(), lse.data_ptr(), B, s_q, h_q, kv.shape[1],
+                                   bt.shape[1], SCALE, 1, ns, ws.data_ptr(), wsb, sp) == 0
+    if ns > 1:
+        assert capi.mla_combine_launch(ws.data_ptr(), wsb, out.data_ptr(), lse.data_ptr(), B, s_q,
+                                       h_q, ns, sp) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, want[0]) and torch.equal(lse, want[1])
+
+
+@pytest.mark.parametrize("ns", [1, 3])
+def test_late_dominant_key(gpu, ns):
+    # A key far above everything before it (score ~ 2|q|^2, ~70 in log2
+    # units above the first tiles' maxima) makes its rows' first-tile
+    # reference too small: the split is run again against the true maxima.
+    # Other rows get a dominant key in their first tile (no second pass
+    # needed), and request 1 none at all.
+    case = mla_case([700, 300, 95], 1, 64, seed=11)
+    q, kv, bt, sl = case
+    bs = kv.shape[1]
+    for row, tok in ((5, 400), (40, 690), (63, 33)):
+        blk, slot = int(bt[0, tok // bs]), tok % bs
+        kv[blk, slot, 0] = (q[0, 0, row].float() * 2).to(torch.bfloat16)
+    blk = int(bt[2, 2 // bs])
+    kv[blk, 2 % bs, 0] = (q[2, 0, 7].float() * 2).to(torch.bfloat16)
+    for causal in (False, True):
+        check(run(case, causal, ns), oracle(case, causal), f"dominant/ns{ns}/c{causal}")
+
+
+# --------------------------------------------------------- token-balanced launch
+
+
+def run_balanced(case, causal, nwg):
+    q, kv, bt, sl = case
+    B, s_q, h_q, _ = q.shape
+    out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, h_q, s_q, dtype=torch.float32, device=q.device)
+    wsb = capi.mla_balanced_workspace_bytes(B, s_q, h_q, nwg)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
+    rc = capi.mla_balanced_launch(q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                  out.data_ptr(), lse.data_ptr(), B, s_q, h_q, kv.shape[1],
+                                  bt.shape[1], SCALE, int(causal), nwg, ws.data_ptr(), wsb,
+                                  torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return out, lse
+
+
+@pytest.mark.parametrize("s_q", [1, 2])
+@pytest.mark.parametrize("h_q", [16, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_balanced_flashmla_grid(gpu, s_q, h_q, causal):
+    S_list = mla_seq_lens(6, 900, seed=h_q + 1, s_q=s_q)
+    print(f"balanced s_q={s_q} h_q={h_q} causal={causal} S={S_list}", flush=True)
+    case = mla_case(S_list, s_q, h_q, seed=h_q + s_q + 1)
+    want = oracle(case, causal)
+    for nwg in (1, 5, 64, 256):
+        check(run_balanced(case, causal, nwg), want, f"bal s_q{s_q}/h{h_q}/c{causal}/n{nwg}")
+
+
+@pytest.mark.parametrize("S_list", [[0], [0, 0, 5], [1, 0, 64, 65, 0, 33], [3000], [31, 32, 33],
+                                    [0, 2000, 0, 1, 700]])
+def test_balanced_ragged_and_empty(gpu, S_list):
+    # Empty requests, one-token requests, one long request over every share,
+    # and share counts below, at and above the tile count.
+    case = mla_case(S_list, 2, 16, seed=len(S_list))
+    tiles = sum(-(-s // 32) for s in S_list)
+    for causal in (False, True):
+        want = oracle(case, causal)
+        for nwg in sorted({1, 2, max(1, tiles), tiles + 3, 97}):
+            check(run_balanced(case, causal, nwg), want, f"{S_list}/c{causal}/n{nwg}")
+
+
+@pytest.mark.parametrize("bs", [16, 48, 128])
+def test_balanced_block_sizes(gpu, bs):
+    case = mla_case([1, 200, 333, 64, 900], 1, 64, bs=bs, seed=bs + 1)
+    want = oracle(case, False)
+    for nwg in (3, 17):
+        check(run_balanced(case, False, nwg), want, f"bal bs{bs}/n{nwg}")
+
+
+@pytest.mark.parametrize("h_q", [33, 200, 256])
+def test_balanced_row_groups(gpu, h_q):
+    # Rows past one 128-row group: one set of shares per row group.
+    case = mla_case([300, 1, 129, 500], 1, h_q, seed=h_q + 2)
+    want = oracle(case, True)
+    for nwg in (4, 24):
+        check(run_balanced(case, True, nwg), want, f"bal h{h_q}/n{nwg}")
+
+
+def test_balanced_repeatable_and_close_to_split(gpu):
+    case = mla_case(mla_seq_lens(9, 1500, seed=8), 1, 128, seed=8)
+    first = run_balanced(case, False, 40)
+    for _ in range(3):
+        again = run_balanced(case, False, 40)
+        assert torch.equal(again[0], first[0]) and torch.equal(again[1], first[1])
+    split = run(case, False, 4)
+    assert torch.allclose(first[0].float(), split[0].float(), atol=2e-2, rtol=2e-2)
+    fin = torch.isfinite(split[1])
+    assert torch.allclose(first[1][fin], split[1][fin], atol=5e-3)
+
+
+def test_balanced_late_dominant_key(gpu):
+    case = mla_case([700, 300, 95], 1, 64, seed=11)
+    q, kv, bt, sl = case
+    bs = kv.shape[1]
+    for row, tok in ((5, 400), (40, 690), (63, 33)):
+        blk, slot = int(bt[0, tok // bs]), tok % bs
+        kv[blk, slot, 0] = (q[0, 0, row].float() * 2).to(torch.bfloat16)
+    want = oracle(case, False)
+    for nwg in (1, 4, 9):
+        check(run_balanced(case, False, nwg), want, f"bal dominant/n{nwg}")
+
+
+def test_balanced_benchmark_batch(gpu):
+    cfg = MLA_CONFIGS["mla_4k"]
+    S_list = mla_seq_lens(cfg["B"], cfg["S_mean"], seed=0)
+    case = make_mla_case(S_list, cfg["s_q"], cfg["h_q"], cfg["bs"], pool_factor=1.1, seed=0,
+                         device="cuda")
+    rows = [0, 17, 40, 63, 64, 99, 120, 127]
+    check(run_balanced(case, False, 256), oracle(case, False, rows), "bal mla_4k", rows=rows)

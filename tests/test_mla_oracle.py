@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import make_mla_case
+from cases import make_mla_case, mla_flops_bytes
 from oracle import c_oracle
 from oracle import mla_reference as mref
 from oracle.reference import bf16_to_f32
@@ -199,8 +199,19 @@ def test_planted_mistake_is_caught(monkeypatch):
 
 
 def test_flops_bytes_accounting():
-    # FlashMLA's counting for b=128, s_q=1, h_q=128, every request at 32768:
+    # The benchmark's accounting (bench/cases.py), FlashMLA's counting for b=128, s_q=1, h_q=128, every request at 32768:
     # 128*128*32768*2*(576+512) FLOPs; bytes = q + latent rows once + out.
-    flops, nbytes = mref.mla_flops_bytes([32768] * 128, 1, 128)
+    flops, nbytes = mla_flops_bytes([32768] * 128, 1, 128)
     assert flops == 2.0 * 128 * 128 * 32768 * 1088
     assert nbytes == 128 * 128 * 576 * 2 + 128 * 32768 * 576 * 2 + 128 * 128 * 512 * 2
+
+
+@pytest.mark.parametrize("s_q,s_k,tflops,gbps", [
+    (1, 4096, 535, 2344), (1, 8192, 583, 2480), (1, 16384, 610, 2561), (1, 32768, 627, 2612),
+    (2, 4096, 690, 1595), (2, 8192, 729, 1597), (2, 16384, 751, 1598), (2, 32768, 758, 1592)])
+def test_accounting_matches_flashmla_log(s_q, s_k, tflops, gbps):
+    # FlashMLA's printed rows (docs/g0/flashmla_bench_raw.txt:4675-4697 of the
+    # reference) fix the ratio of its byte count to its FLOP count, whatever
+    # the varlen draw's total: both counts must be the ones it used.
+    flops, nbytes = mla_flops_bytes([s_k] * 128, s_q, 128)
+    assert abs((nbytes / flops) / (gbps / (tflops * 1e3)) - 1) < 0.01
