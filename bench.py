@@ -437,7 +437,8 @@ def main_mla(args, dev, props):
                      "peak": peak, "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
                      "frac": round(achieved / peak, 4), "avg_kernel_us": round(kern_us, 3),
                      "mfma_frac": round(tflops_k * 1e12 / MFMA_BF16_PEAK, 4),
-                     "hbm_frac": round(gbps_k * 1e9 / HBM_PEAK, 4), "traffic": None},
+                     "hbm_frac": round(gbps_k * 1e9 / HBM_PEAK, 4),
+                     "traffic": read_traffic(args.config, "mla", "balanced" if balanced else ns)},
         "device": props.name, "gcn_arch": props.gcnArchName, "cus": props.multi_processor_count,
         "clocks": cases.gpu_clocks(),
     }

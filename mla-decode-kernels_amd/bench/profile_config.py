@@ -102,7 +102,10 @@ def read_csvs(directory, suffix):
     return rows
 
 
-def kernel_durations(directory, pattern="gqa"):
+MLA_CONFIGS = [f"mla_{k}k{sfx}" for sfx in ("", "_sq2") for k in (4, 8, 16, 32)]
+
+
+def kernel_durations(directory, pattern="gqa|mla"):
     """{kernel: [durations in us]} from a --kernel-trace pass."""
     out = {}
     for r in read_csvs(directory, "kernel_trace.csv"):
@@ -113,7 +116,7 @@ def kernel_durations(directory, pattern="gqa"):
     return out
 
 
-def counter_means(directory, pattern="gqa|neg_kernel"):
+def counter_means(directory, pattern="gqa|mla|neg_kernel"):
     """{(kernel, counter): mean value over dispatches} from a --pmc pass."""
     acc = {}
     for r in read_csvs(directory, "counter_collection.csv"):
@@ -175,14 +178,16 @@ def traffic_line(root, config, traffic):
     for f in out:
         for line in open(f):
             if line.startswith("{") and '"metric"' in line:
-                split = json.loads(line)["config"]["num_splits"]
-    kernel = "v2"
+                cfg = json.loads(line)["config"]
+                split = cfg.get("num_splits", cfg.get("launch"))
+    kernel = "mla" if config.startswith("mla") else "v2"
     return f"{config} {kernel} {split} {traffic[0]} {traffic[1]}" if split is not None else None
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5"] + MLA_CONFIGS)
     ap.add_argument("--out-dir", default=None)
     ap.add_argument("--passes", default=",".join(PASSES))
     ap.add_argument("--timeout", type=int, default=300, help="seconds per pass")

@@ -4,24 +4,31 @@
 // dims. Semantics and layouts: include/mla_decode.h.
 //
 // Work decomposition. A workgroup of 4 waves (one per SIMD) owns 128 query
-// rows of one request and one split of its tokens; each wave owns 32 rows as
-// two 16-row MFMA column blocks. All rows share the cache rows, so each
-// 32-token tile (36 KiB) is read from HBM once per workgroup: the waves load it
-// cooperatively into registers, one tile ahead, and store it into one of two
-// LDS buffers, then every wave computes from LDS.
+// rows (a row group) of one request and a range of its tokens; each wave owns
+// 32 rows as two 16-row MFMA column blocks. All rows share the cache rows, so
+// each 32-token tile (36 KiB) is read from HBM once per workgroup: the waves
+// copy it cooperatively, HBM -> LDS (global_load_lds_dwordx4, no registers),
+// into a ring of kDepth slots with kDepth - 1 tiles in flight, and every wave
+// computes from LDS. Two launches share this tile walk (mla_piece):
+//   fixed splits  grid (row groups, B, num_splits), split s of each request;
+//   balanced      one workgroup per CU and row group, each taking an equal
+//                 share of the batch's request-ordered tiles (a plan kernel
+//                 computes the tile prefix sums on the device), walked piece
+//                 by piece; requests cut between shares are merged after.
 //
-// LDS tile layout ("A order"): 36 blocks of 1 KiB, block (tg, kk) for token
-// group tg (16 tokens) and 32-dim k-step kk holds, at 16 * lane, the 16 bytes
-// lane (j = lane % 16, g = lane / 16) needs as the A operand of
-// v_mfma_f32_16x16x32_bf16: token 16 tg + j, dims 32 kk + 8 g .. +8. A wave's
-// staging loads and stores fill whole blocks (contiguous 1 KiB stores), and
-// the QK operand reads are contiguous too.
+// LDS tile layout ("A order", swizzled): 36 blocks of 1 KiB, block (tg, kk)
+// for token group tg (16 tokens) and 32-dim k-step kk; within a block the
+// 16-byte slot of token t16 and dims 8q .. 8q + 8 is 16 q + (t16 ^ 8 (q & 1)).
+// Lane (j = lane % 16, g = lane / 16) of a copy fills slot 16 g + j, so whole
+// 1 KiB blocks are written; the swizzle spreads the transposing PV reads over
+// all LDS banks.
 //
 //   QK^T   S^T[16 tok x 16 rows] = K[tok x 576] . Q^T[576 x 16 rows]: 18
 //          MFMAs per token group and row block; A from LDS (shared by both
 //          row blocks), B = Q^T in registers (lane: row j, dims 32 kk + 8 g).
-//   softmax on the C layout (lane: row j, tokens 4 g + e), base 2, fp32
-//          state; P rounded to bf16, l sums the rounded values.
+//   softmax on the C layout (lane: row j, tokens 4 g + e), base 2, fp32,
+//          against a per-row reference max fixed at the row's first live
+//          tile (see kRefSlack); P rounded to bf16, l sums the rounded values.
 //   PV     O[16 rows x 512] += P[rows x 32 tok] . V[32 tok x 512]: 32
 //          v_mfma_f32_16x16x32_bf16 per row block (k-slot 8g+e -> token
 //          4g+e, 8g+4+e -> token 16+4g+e); B read from the same LDS tile with
@@ -29,8 +36,8 @@
 //          4g + x/4, dims 16nb + 4(x%4) .. +4; the transpose hands lane x the
 //          four tokens of dim 16nb + x).
 //
-// Splits cut a request at multiples of 32 tokens; a merge kernel folds them
-// in split order (log-sum-exp), so results are bitwise reproducible.
+// Splits and shares cut requests at multiples of 32 tokens; the merges fold
+// the pieces in order (log-sum-exp), so results are bitwise reproducible.
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
 #include "mla_decode.h"

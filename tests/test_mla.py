@@ -134,11 +134,22 @@ def test_python_surface(gpu):
     # FlashMLA-style calls: metadata, then the decode with the default scale.
     case = mla_case(mla_seq_lens(6, 1500, seed=4, s_q=2), 2, 32, seed=4)
     q, kv, bt, sl = case
+    want = oracle(case, True)
     meta, splits = get_mla_metadata(sl, 2 * 32, 1)
-    assert splits.shape == (7,) and int(meta[0, 0]) >= 1
+    assert meta.device.type == "cpu" and int(meta[0, 0]) == 0 and int(meta[0, 1]) > 0
+    assert splits.shape == (7,) and int(splits[-1]) >= int((sl > 0).sum())
     out, lse = flash_mla_with_kvcache(q, kv, bt, sl, 512, meta, splits, causal=True)
     torch.cuda.synchronize()
-    check((out, lse), oracle(case, True), "flash_mla_with_kvcache")
+    check((out, lse), want, "flash_mla_with_kvcache balanced")
+    for n in (0, 3):
+        meta, splits = get_mla_metadata(sl, 2 * 32, 1, num_splits=n)
+        assert int(meta[0, 0]) >= 1
+        out, lse = flash_mla_with_kvcache(q, kv, bt, sl, 512, meta, splits, causal=True)
+        torch.cuda.synchronize()
+        check((out, lse), want, f"flash_mla_with_kvcache splits={n}")
+    out, lse = flash_mla_with_kvcache(q, kv, bt, sl, 512, causal=True)
+    torch.cuda.synchronize()
+    check((out, lse), want, "flash_mla_with_kvcache default")
     with pytest.raises(ValueError):
         flash_mla_with_kvcache(q.float(), kv, bt, sl, 512)
     with pytest.raises(ValueError):
