@@ -228,6 +228,39 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
   // token instead (masked later), so nothing outside the request's live cache
   // rows is touched. Block ids come from scalar loads, which keeps the vector
   // memory counter for the copies alone.
+  // The refill copies of the block-uniform path are issued two per QK^T
+  // k-step rather than in one burst after the barrier (a burst queues behind
+  // the other waves' copies and holds the wave); Plan carries what they need,
+  // and the block id is loaded one iteration ahead, before the barrier, so
+  // that its scalar-load latency overlaps the wait for the landing tile.
+  struct Plan {
+    const uint16_t* base;
+    uint32_t voff[2];
+    uint32_t slot;
+  };
+  auto block_id = [&](int k) -> int {
+    return btc[gqa::fastdiv((uint32_t)(seg_start + kTile * k), a.bs_div)];
+  };
+  auto prep = [&](int k, int id) -> Plan {
+    const int ts = seg_start + kTile * k;
+    Plan p;
+    p.slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
+    int tok[2];
+#pragma unroll
+    for (int tg = 0; tg < 2; ++tg) tok[tg] = ts + 16 * tg + js < seg_end ? 16 * tg + js : 0;
+    const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
+    const size_t row0 = (size_t)id * bs + (ts - (int)lb * bs);
+    p.base = a.kv + row0 * kD;
+#pragma unroll
+    for (int tg = 0; tg < 2; ++tg) p.voff[tg] = (uint32_t)(tok[tg] * kD + 8 * g) * 2u;
+    return p;
+  };
+  auto issue = [&](const Plan& p, int i) {
+    const int blk = w + kWaves * i;
+    const int tg = blk >= kKSteps ? 1 : 0, kk = blk - tg * kKSteps;
+    load_to_lds(p.base + 32 * kk, tg ? p.voff[1] : p.voff[0],
+                __builtin_amdgcn_readfirstlane(p.slot + (uint32_t)blk * 1024));
+  };
   auto stage = [&](int k) {
     const int ts = seg_start + kTile * k;
     const uint32_t slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
@@ -292,6 +325,10 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
 #pragma unroll
       for (int nb = 0; nb < kNB; ++nb) o[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    int id_next = 0;
+    if constexpr (kBlockUniform) {
+      if (kDepth - 1 < ntiles) id_next = block_id(kDepth - 1);
+    }
     // Prologue: tiles 0 .. kDepth - 2 in flight; tile 0 published.
     for (int k = 0; k < kDepth - 1 && k < ntiles; ++k) stage(k);
     if (ntiles >= kDepth - 1)
@@ -302,7 +339,12 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
       // Refill the slot consumed in the previous iteration (every wave has
       // passed the barrier that ended it).
       const bool refill = k + kDepth - 1 < ntiles;
-      if (refill) stage(k + kDepth - 1);
+      Plan pl;
+      if constexpr (kBlockUniform) {
+        if (refill) pl = prep(k + kDepth - 1, id_next);
+      } else {
+        if (refill) stage(k + kDepth - 1);
+      }
       const uint8_t* T = tiles[k % kDepth];
       const int ts = seg_start + kTile * k;
 
@@ -328,6 +370,9 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
           const int sl = (kk + kQKAhead) % (kQKAhead + 1);
 #pragma unroll
           for (int x = 0; x < 2; ++x) kr[sl][x] = read_k(kk + kQKAhead, x);
+        }
+        if constexpr (kBlockUniform) {
+          if ((kk & 1) == 0 && refill) issue(pl, kk >> 1);  // copies 0..8 of the refill
         }
         __builtin_amdgcn_sched_barrier(0);
         const int sl = kk % (kQKAhead + 1);
@@ -411,6 +456,11 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
                                                               o[rb][nb], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
+      }
+      // The block id the next iteration's copies need, loaded here so that
+      // its latency overlaps the wait below.
+      if constexpr (kBlockUniform) {
+        if (k + kDepth < ntiles) id_next = block_id(k + kDepth);
       }
       // Tile k + 1 must have landed; the later ones stay in flight.
       if (refill)
