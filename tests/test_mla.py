@@ -301,3 +301,44 @@ def test_balanced_benchmark_batch(gpu):
                          device="cuda")
     rows = [0, 17, 40, 63, 64, 99, 120, 127]
     check(run_balanced(case, False, 256), oracle(case, False, rows), "bal mla_4k", rows=rows)
+
+
+def test_balanced_graph_replay(gpu):
+    # The balanced launch (plan, split, merge: no host sync, no memset) inside a
+    # HIP graph: every replay, with eager work between, equals the eager run.
+    case = mla_case(mla_seq_lens(5, 800, seed=12, s_q=2), 2, 32, seed=12)
+    q, kv, bt, sl = case
+    B, s_q, h_q, _ = q.shape
+    want = run_balanced(case, True, 24)
+    out = torch.empty_like(want[0])
+    lse = torch.empty_like(want[1])
+    wsb = capi.mla_balanced_workspace_bytes(B, s_q, h_q, 24)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device)
+    s = torch.cuda.Stream()
+    args = lambda st: (q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(),  # noqa: E731
+                       out.data_ptr(), lse.data_ptr(), B, s_q, h_q, kv.shape[1], bt.shape[1],
+                       SCALE, 1, 24, ws.data_ptr(), wsb, st.cuda_stream)
+    with torch.cuda.stream(s):
+        assert capi.mla_balanced_launch(*args(s)) == 0  # warm-up on the capture stream
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        assert capi.mla_balanced_launch(*args(s)) == 0
+    for rep in range(4):
+        out.zero_()
+        lse.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want[0]) and torch.equal(lse, want[1]), f"replay {rep}"
+        run_balanced(case, False, 7)  # eager work between replays
+
+
+def test_balanced_many_requests(gpu):
+    # 3000 short requests (the plan kernel's scan then takes several requests
+    # per thread), checked on a subset.
+    S_list = [(7 * i) % 97 for i in range(3000)]
+    case = make_mla_case(S_list, 1, 16, 16, pool_factor=1.0, seed=13, device="cuda")
+    got = run_balanced(case, False, 256)
+    rows = [0, 1, 2, 500, 1499, 2998, 2999]
+    check(got, oracle(case, False, rows), "bal many", rows=rows)
