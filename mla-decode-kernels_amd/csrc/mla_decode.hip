@@ -126,6 +126,10 @@ constexpr int kPVAhead = 4;
 // completion is awaited explicitly with s_waitcnt vmcnt before the barrier
 // that publishes a tile. The first form addresses base + voff (a uniform
 // 64-bit base, a 32-bit per-lane offset); the second a per-lane address.
+// M0 is a register the compiler reserves (hipcc notes the clobber as such and
+// will not restore it): these kernels rely on the compiler emitting no M0 use
+// of its own, which tests/test_mla_codegen.py checks on the generated code,
+// together with the spill-free and wait-free tile loops.
 __device__ __forceinline__ void load_to_lds(const uint16_t* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                :

@@ -1,0 +1,84 @@
+"""Code-generation checks of the MLA decode kernels (CPU: hipcc cross-compiles
+csrc/mla_decode.hip for gfx950 to assembly).
+
+The kernels' speed rests on properties of the generated code that a compiler
+change or an innocent-looking edit can silently break, so they are checked here:
+  - no scratch (spill) access inside the tile loops: the 256 accumulators fill
+    the accumulation registers, and a spill reload waits for every HBM->LDS
+    copy in flight;
+  - no compiler-inserted vmcnt wait inside the tile loops (the copies are
+    awaited only by the kernel's own s_waitcnt before each barrier);
+  - no compiler use of M0: the copies set M0 in inline assembly, and M0 is a
+    register the compiler reserves (it would not restore it).
+"""
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "mla-decode-kernels_amd", "csrc", "mla_decode.hip")
+HIPCC = "/opt/rocm/bin/hipcc"
+
+pytestmark = pytest.mark.skipif(not shutil.which(HIPCC), reason="hipcc not available")
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    out = tmp_path_factory.mktemp("mla_asm") / "mla_decode.s"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang",
+                    "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                    f"-I{os.path.join(ROOT, 'include')}",
+                    f"-I{os.path.join(ROOT, 'mla-decode-kernels_amd', 'csrc')}", SRC, "-o",
+                    str(out)], check=True, capture_output=True)
+    return out.read_text()
+
+
+def kernel_body(asm, mangled):
+    start = asm.index(f"\n{mangled}:")
+    return asm[start:asm.index("s_endpgm", start)]
+
+
+def tile_loops(body):
+    """(text of each loop that issues MFMAs, from its header to its first
+    barrier)."""
+    lines = body.split("\n")
+    loops = []
+    for i, ln in enumerate(lines):
+        if "Loop Header" in ln:
+            for k in range(i + 1, len(lines)):
+                if "s_barrier" in lines[k]:
+                    text = "\n".join(lines[i:k])
+                    if "v_mfma" in text:
+                        loops.append(text)
+                    break
+    return loops
+
+
+KERNELS = ["_ZN3mla17mla_decode_kernelILb1EEEvNS_7MlaArgsE",
+           "_ZN3mla17mla_decode_kernelILb0EEEvNS_7MlaArgsE",
+           "_ZN3mla26mla_decode_balanced_kernelILb1EEEvNS_7MlaArgsE",
+           "_ZN3mla26mla_decode_balanced_kernelILb0EEEvNS_7MlaArgsE"]
+
+
+@pytest.mark.parametrize("mangled", KERNELS)
+def test_tile_loops_clean(asm, mangled):
+    loops = tile_loops(kernel_body(asm, mangled))
+    assert loops, "no tile loop found"
+    for text in loops:
+        code = [ln for ln in text.split("\n") if ln.strip() and not ln.strip().startswith(";")]
+        assert not [ln for ln in code if "scratch_" in ln], "spill access inside a tile loop"
+        # Waits the compiler inserted (outside the ;;#ASMSTART blocks) must
+        # not name vmcnt.
+        own = re.sub(r";;#ASMSTART.*?(;;#ASMEND|\Z)", "", text, flags=re.S)
+        assert "vmcnt" not in own, "compiler vmcnt wait inside a tile loop"
+        assert text.count("v_mfma_f32_16x16x32_bf16") == 136
+
+
+@pytest.mark.parametrize("mangled", KERNELS)
+def test_m0_only_in_inline_asm(asm, mangled):
+    outside = re.sub(r";;#ASMSTART.*?;;#ASMEND", "", kernel_body(asm, mangled), flags=re.S)
+    assert not re.search(r"\bm0\b", outside)
