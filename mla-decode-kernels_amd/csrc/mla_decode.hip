@@ -126,18 +126,20 @@ constexpr int kPVAhead = 4;
 // completion is awaited explicitly with s_waitcnt vmcnt before the barrier
 // that publishes a tile. The first form addresses base + voff (a uniform
 // 64-bit base, a 32-bit per-lane offset); the second a per-lane address.
+// The s_nop separates the SALU write of M0 from its read by the copy (the
+// compiler's hazard recognizer does not look inside inline assembly).
 // M0 is a register the compiler reserves (hipcc notes the clobber as such and
 // will not restore it): these kernels rely on the compiler emitting no M0 use
 // of its own, which tests/test_mla_codegen.py checks on the generated code,
 // together with the spill-free and wait-free tile loops.
 __device__ __forceinline__ void load_to_lds(const uint16_t* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                :
                : "v"(voff), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 __device__ __forceinline__ void load_to_lds(const uint16_t* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
                :
                : "v"(src), "s"(lds)
                : "memory", "m0");
