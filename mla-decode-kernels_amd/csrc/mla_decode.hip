@@ -126,8 +126,10 @@ constexpr int kPVAhead = 4;
 // completion is awaited explicitly with s_waitcnt vmcnt before the barrier
 // that publishes a tile. The first form addresses base + voff (a uniform
 // 64-bit base, a 32-bit per-lane offset); the second a per-lane address.
-// The s_nop separates the SALU write of M0 from its read by the copy (the
-// compiler's hazard recognizer does not look inside inline assembly).
+// On gfx9-family GPUs an LDS-DMA instruction needs one wait state after an
+// SALU write of M0; the compiler inserts it for its own LDS-DMA code but does
+// not look inside inline assembly, hence the s_nop (measured cost: up to ~3 %
+// on the matrix-bound s_q = 2 workloads).
 // M0 is a register the compiler reserves (hipcc notes the clobber as such and
 // will not restore it): these kernels rely on the compiler emitting no M0 use
 // of its own, which tests/test_mla_codegen.py checks on the generated code,
