@@ -104,10 +104,10 @@ def test_short_and_empty(gpu, S_list, ns):
         check(run(case, causal, ns), oracle(case, causal), f"{S_list}/ns{ns}/c{causal}")
 
 
-@pytest.mark.parametrize("bs", [16, 32, 128, 7, 48])
+@pytest.mark.parametrize("bs", [16, 32, 128, 7, 48, 1, 3])
 def test_block_sizes(gpu, bs):
     # Multiples of 32 keep a tile inside one block (scalar block id); others
-    # take the per-lane gather.
+    # take the per-lane gather (block 1: a tile spans 32 blocks).
     case = mla_case([1, 200, 333, 64], 1, 64, bs=bs, seed=bs)
     for ns in (1, 4):
         check(run(case, False, ns), oracle(case, False), f"bs{bs}/ns{ns}")
@@ -253,7 +253,7 @@ def test_balanced_ragged_and_empty(gpu, S_list):
             check(run_balanced(case, causal, nwg), want, f"{S_list}/c{causal}/n{nwg}")
 
 
-@pytest.mark.parametrize("bs", [16, 48, 128])
+@pytest.mark.parametrize("bs", [16, 48, 128, 1])
 def test_balanced_block_sizes(gpu, bs):
     case = mla_case([1, 200, 333, 64, 900], 1, 64, bs=bs, seed=bs + 1)
     want = oracle(case, False)
