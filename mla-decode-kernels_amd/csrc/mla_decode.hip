@@ -159,14 +159,19 @@ __device__ __forceinline__ void publish_barrier() {
 // Max over lanes l, l ^ 16, l ^ 32 and l ^ 48, the four lanes that hold one
 // row in the MFMA C layout: v_permlane16_swap (v_permlane32_swap) with both
 // operands x hands every lane x of itself and of its xor-16 (xor-32) partner,
-// in VALU registers (no LDS round trip).
+// in VALU registers (no LDS round trip). The two results are copied out of the
+// builtin's vector as plain integers before any bit cast: this clang lowers
+// __builtin_bit_cast of an element (b[1]) as a read of element 0, which drops
+// the partner's value and with it the max.
 __device__ __forceinline__ float row_max(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const uint32_t u = __float_as_uint(x);
   const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float y = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
-  const uint32_t v = __builtin_bit_cast(uint32_t, y);
+  const uint32_t a0 = a[0], a1 = a[1];
+  const float y = fmaxf(__uint_as_float(a0), __uint_as_float(a1));
+  const uint32_t v = __float_as_uint(y);
   const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__builtin_bit_cast(float, b[0]), __builtin_bit_cast(float, b[1]));
+  const uint32_t b0 = b[0], b1 = b[1];
+  return fmaxf(__uint_as_float(b0), __uint_as_float(b1));
 }
 
 // Where a piece's results go: normalised rows to out and lse (direct), or
@@ -482,8 +487,11 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
   // A row whose max beat its reference by more than kRefSlack has overflowed
   // or lost precision: the workgroup (which stages tiles together) runs the
   // split again with every row's reference at its true max (probabilities
-  // <= 1, so a second pass always suffices).
-  if (lane == 0) restart_vote[w] = __builtin_amdgcn_ballot_w64(beaten) != 0;
+  // <= 1, so a second pass always suffices). The ballot is taken with the
+  // whole wave active (each lane holds its own rows' and tokens' flag); only
+  // the store is lane 0's.
+  const bool wave_beaten = __builtin_amdgcn_ballot_w64(beaten) != 0;
+  if (lane == 0) restart_vote[w] = wave_beaten;
   __syncthreads();
   if (restart_vote[0] | restart_vote[1] | restart_vote[2] | restart_vote[3]) {
 #pragma unroll
@@ -745,8 +753,8 @@ extern "C" int mla_decode_pick_num_splits(int B, int s_q, int h_q, int block_siz
   constexpr int64_t kMinChunk = 256;
   if (B < 1 || s_q < 1 || h_q < 1 || block_size < 1 || max_blocks < 1) return 0;
   if (num_cus <= 0 && (num_cus = gqa::device_cu_count()) <= 0) return 0;
-  const int64_t groups = (int64_t)B * ((int64_t)s_q * h_q + mla::kRowsPerGroup - 1) /
-                         mla::kRowsPerGroup;
+  const int64_t groups =
+      (int64_t)B * (((int64_t)s_q * h_q + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup);
   int64_t ns = (num_cus + groups - 1) / groups;
   const int64_t s_max = (int64_t)max_blocks * block_size;
   ns = std::min<int64_t>(ns, std::max<int64_t>(1, s_max / kMinChunk));

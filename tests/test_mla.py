@@ -193,10 +193,12 @@ def test_split_and_combine_launches(gpu, ns):
 @pytest.mark.parametrize("ns", [1, 3])
 def test_late_dominant_key(gpu, ns):
     # A key far above everything before it (score ~ 2|q|^2, ~70 in log2
-    # units above the first tiles' maxima) makes its rows' first-tile
-    # reference too small: the split is run again against the true maxima.
-    # Other rows get a dominant key in their first tile (no second pass
-    # needed), and request 1 none at all.
+    # units above the first tiles' maxima, past the 32-unit slack of the
+    # first-tile reference but not past fp32's range): the workgroup runs its
+    # split a second time against the true maxima. Other rows get a dominant
+    # key in their first tile (no second pass needed), and request 1 none at
+    # all. test_overflowing_late_key plants keys that would overflow without
+    # the second pass.
     case = mla_case([700, 300, 95], 1, 64, seed=11)
     q, kv, bt, sl = case
     bs = kv.shape[1]
@@ -207,6 +209,57 @@ def test_late_dominant_key(gpu, ns):
     kv[blk, 2 % bs, 0] = (q[2, 0, 7].float() * 2).to(torch.bfloat16)
     for causal in (False, True):
         check(run(case, causal, ns), oracle(case, causal), f"dominant/ns{ns}/c{causal}")
+
+
+# Keys 5 q (score 5 |q|^2 / 24, ~170 log2 units) planted at (row, token) of
+# request 0, in rows other than row 0 of their 16-row MFMA block and at tokens
+# outside lane 0's score slots (lane (j, g) holds row j's tokens 16 tg + 4 g +
+# e of a tile): a restart vote read from lane 0 alone would miss all of them.
+OVERFLOW_PLANTS = ((5, 405), (40, 694), (63, 45), (97, 301))
+
+
+def overflow_case():
+    case = mla_case([700, 300, 95], 1, 128, seed=13)
+    q, kv, bt, sl = case
+    bs = kv.shape[1]
+    for row, tok in OVERFLOW_PLANTS:
+        assert row % 16 != 0 and (tok % 16) // 4 != 0
+        kv[int(bt[0, tok // bs]), tok % bs, 0] = (q[0, 0, row].float() * 5).to(torch.bfloat16)
+    # Each planted score beats every other key of its row by more than 128
+    # log2 units: against any reference not set by the planted key itself,
+    # exp2 overflows fp32, so a finite, correct result needs the second pass.
+    qh = q[0, 0].float().cpu().double().numpy()
+    keys = torch.stack([kv[int(bt[0, t // bs]), t % bs, 0] for t in range(700)]).float()
+    sc = (qh @ keys.cpu().double().numpy().T) * SCALE / np.log(2.0)
+    for row, tok in OVERFLOW_PLANTS:
+        assert sc[row, tok] - np.delete(sc[row], tok).max() > 128.0
+    return case
+
+
+def split_first_tile(tok, S, ns):
+    """First tile (in tokens) of the fixed split holding token tok."""
+    chunk = (-(-S // ns) + 31) // 32 * 32
+    return tok // chunk * chunk
+
+
+def share_first_tile(tok, tiles_before, T, n):
+    """First tile (in tokens, request-relative) of the balanced piece holding
+    token tok of a request whose tiles start at tiles_before."""
+    n = min(n, T)
+    t = tiles_before + tok // 32
+    w = max(w for w in range(n) if w * T // n <= t)
+    return (max(w * T // n, tiles_before) - tiles_before) * 32
+
+
+@pytest.mark.parametrize("ns", [1, 3, 5])
+def test_overflowing_late_key(gpu, ns):
+    case = overflow_case()
+    for _, tok in OVERFLOW_PLANTS:
+        assert tok // 32 * 32 != split_first_tile(tok, 700, ns), "plant sets its reference"
+    for causal in (False, True):
+        got = run(case, causal, ns)
+        assert torch.isfinite(got[0].float()).all()
+        check(got, oracle(case, causal), f"overflow/ns{ns}/c{causal}")
 
 
 # --------------------------------------------------------- token-balanced launch
@@ -342,3 +395,15 @@ def test_balanced_many_requests(gpu):
     got = run_balanced(case, False, 256)
     rows = [0, 1, 2, 500, 1499, 2998, 2999]
     check(got, oracle(case, False, rows), "bal many", rows=rows)
+
+
+def test_balanced_overflowing_late_key(gpu):
+    case = overflow_case()
+    T = sum(-(-x // 32) for x in (700, 300, 95))
+    want = oracle(case, False)
+    for nwg in (1, 4, 9):
+        for _, tok in OVERFLOW_PLANTS:
+            assert tok // 32 * 32 != share_first_tile(tok, 0, T, nwg), "plant sets its reference"
+        got = run_balanced(case, False, nwg)
+        assert torch.isfinite(got[0].float()).all()
+        check(got, want, f"bal overflow/n{nwg}")

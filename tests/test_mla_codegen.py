@@ -82,3 +82,49 @@ def test_tile_loops_clean(asm, mangled):
 def test_m0_only_in_inline_asm(asm, mangled):
     outside = re.sub(r";;#ASMSTART.*?;;#ASMEND", "", kernel_body(asm, mangled), flags=re.S)
     assert not re.search(r"\bm0\b", outside)
+
+
+# LDS byte offset of the restart votes: they follow the kDepth x 36 KiB tile ring.
+VOTE_LDS = "0x24000"
+
+
+@pytest.mark.parametrize("mangled", KERNELS)
+def test_restart_ballot_sees_every_lane(asm, mangled):
+    # The second-pass vote is a ballot over the wave's `beaten` flags, stored
+    # by lane 0. The ballot (a v_cmp into vcc) must be evaluated before the
+    # lane-0 branch narrows the exec mask: inside it, it would see lane 0 only.
+    lines = kernel_body(asm, mangled).split("\n")
+    stores = [i for i, ln in enumerate(lines)
+              if "ds_write_b32" in ln and any(VOTE_LDS in p for p in lines[max(0, i - 4):i])]
+    assert stores, "restart vote store not found"
+    for i in stores:
+        # The branch narrows exec with s_and_saveexec or by writing exec.
+        k = max(k for k in range(i) if re.search(r"s_and_saveexec|s_(mov|and)_b64 exec,", lines[k]))
+        between = [ln for ln in lines[k:i] if re.search(r"\bv_cmp", ln)]
+        assert not between, f"ballot evaluated under the lane-0 exec mask: {between}"
+        assert any(re.search(r"v_cmp\w*\s+vcc", ln) for ln in lines[max(0, k - 8):k]), \
+            "ballot not found before the lane-0 branch"
+
+
+@pytest.fixture(scope="module")
+def llvm_ir(tmp_path_factory):
+    out = tmp_path_factory.mktemp("mla_ir") / "mla_decode.ll"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang",
+                    "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                    "-emit-llvm", f"-I{os.path.join(ROOT, 'include')}",
+                    f"-I{os.path.join(ROOT, 'mla-decode-kernels_amd', 'csrc')}", SRC, "-o",
+                    str(out)], check=True, capture_output=True)
+    return out.read_text()
+
+
+def test_row_max_uses_both_swap_results(llvm_ir):
+    # row_max: each permlane16/32 swap returns the lane's own value and its
+    # partner's; the max must use both. A front-end lowering of bit casts of
+    # vector elements once read element 0 for both, so the optimised IR kept
+    # only result 0 and the "max" was one lane's value.
+    calls = re.findall(r"(%[\w.]+) = (?:tail )?call \{ i32, i32 \} @llvm\.amdgcn\.permlane(?:16|32)\.swap",
+                       llvm_ir)
+    assert calls, "no permlane swap found"
+    for v in calls:
+        assert re.search(rf"extractvalue \{{ i32, i32 \}} {re.escape(v)}, 1\b", llvm_ir), \
+            f"second result of {v} unused"

@@ -48,3 +48,29 @@ def test_fixed_plan():
     assert int(meta[0, 0]) == 4 and splits.tolist() == [0, 4, 8, 12]
     with pytest.raises(ValueError):
         get_mla_metadata(sl, 128, 2)
+
+
+@pytest.mark.parametrize("B,s_q,h_q,cus,want", [(32, 1, 128, 256, 8), (64, 1, 128, 256, 4),
+                                                (128, 1, 128, 256, 2), (1, 1, 128, 256, 128),
+                                                (8, 2, 128, 256, 16), (3, 1, 200, 256, 43),
+                                                (256, 1, 64, 256, 1), (300, 1, 128, 256, 1)])
+def test_pick_num_splits_covers_cus(B, s_q, h_q, cus, want):
+    # The (row group, request, split) grid covers num_cus workgroups with the
+    # fewest splits: B * ceil(s_q h_q / 128) row groups per split. Long
+    # sequences (1 << 20 tokens), so the 256-token minimum does not bind.
+    import capi
+
+    ns = capi.mla_pick_num_splits(B, s_q, h_q, 64, (1 << 20) // 64, cus)
+    groups = B * -(-(s_q * h_q) // 128)
+    assert ns == want
+    assert ns == 128 or groups * ns >= cus  # 128: MLA_DECODE_MAX_SPLITS
+    assert ns == 1 or groups * (ns - 1) < cus
+
+
+def test_pick_num_splits_min_chunk():
+    import capi
+
+    # 1000 tokens (125 blocks of 8): at most 1000 // 256 = 3 splits, however
+    # few the requests; 128 tokens: one.
+    assert capi.mla_pick_num_splits(1, 1, 128, 8, 125, 256) == 3
+    assert capi.mla_pick_num_splits(1, 1, 128, 64, 2, 256) == 1
