@@ -11,9 +11,8 @@ namespace gqa {
 
 // Split states that another workgroup of the same launch reads (single-launch
 // split mode) are stored and loaded at device scope: the stores write through
-// to the level every XCD reads from, the loads skip stale cached copies. The
-// protocol then needs no cache-wide writeback or invalidate (a device-scope
-// fence does both to the whole L2, which costs more than the merge saves).
+// to the level every XCD reads from, the loads skip cached copies. Their
+// ordering against the arrival count is arrive_last's release/acquire pair.
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -159,25 +158,42 @@ __device__ __forceinline__ void merge_heads4(const float* __restrict__ ws_acc,
 }
 
 // Arrival of a workgroup at the end of its split for merge group `group`, with
-// ns workgroups per group. Every thread waits until its device-scope state
-// stores have completed (s_waitcnt vmcnt(0), gfx9 encoding), the workgroup
-// meets at a barrier, and one thread counts the arrival at device scope. The
-// workgroup that arrives last sets the counter back to zero. Returns, in every
-// thread, whether this workgroup arrived last; its merge loads (issued after
-// the count returned) then see every other workgroup's completed stores.
-// Nothing waits on another workgroup. Call from every thread of the
-// workgroup, after its state stores.
+// ns workgroups per group: the "last workgroup merges" protocol in its
+// textbook form under the HIP (scoped C++) memory model, with each fence
+// placed once.
+//  - Every thread's state stores happen before thread 0's count: each thread
+//    waits for its stores to complete (s_waitcnt vmcnt(0), gfx9 encoding) and
+//    the workgroup meets at a barrier behind a workgroup-scope release fence.
+//  - Thread 0 counts with a release read-modify-write at device (agent)
+//    scope: on gfx950 the compiler emits an L2 writeback (buffer_wbl2 sc1)
+//    and a store wait before the atomic, so the workgroup's states reach the
+//    level every XCD reads before the count can be seen.
+//  - The workgroup that sees ns - 1 arrivals takes an acquire fence at device
+//    scope (buffer_inv sc1: this XCD's L2 drops non-local copies), which
+//    synchronises with every earlier arrival's release; the barrier after it
+//    passes that on to the workgroup's other threads. It sets the counter back
+//    to zero: all ns arrivals of this launch are counted.
+// The states themselves are also stored and loaded at device scope
+// (write-through stores, loads that skip cached copies), so they leave no
+// dirty lines for the writeback. Only one thread per workgroup pays for the
+// writeback and only the last workgroup of a group for the invalidate; a
+// device-scope fence in every wave instead (each would do both) made config 2
+// at 8 splits 3.3x slower. Returns, in every thread, whether this workgroup
+// arrived last. Nothing waits on another workgroup. Call from every thread of
+// the workgroup, after its state stores.
 __device__ __forceinline__ bool arrive_last(uint32_t* counters, size_t group, int ns) {
   __shared__ uint32_t last_flag;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(counters + group, 1u, __ATOMIC_RELAXED,
+    const uint32_t prev = __hip_atomic_fetch_add(counters + group, 1u, __ATOMIC_RELEASE,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     const bool last = prev == (uint32_t)(ns - 1);
-    // All ns arrivals of this launch are counted: the next launch starts at 0.
-    if (last) __hip_atomic_store(counters + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(counters + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     last_flag = last ? 1u : 0u;
   }
   __syncthreads();

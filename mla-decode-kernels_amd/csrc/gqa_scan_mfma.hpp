@@ -18,10 +18,15 @@
 //          MFMAs of 16 dims: v_mfma_f32_16x16x16_bf16 for 16-token tiles
 //          (P is already the A operand: head l%16, tokens 4(l/16)..+3), or
 //          16x16x32 for 32-token tiles under the token permutation
-//          k-slot 8g+e -> token 4g+e, 8g+4+e -> token 16+4g+e. P is rounded
-//          to bf16; the fp32 sum l accumulates the same rounded values, so the
-//          weights stay exactly normalised (each differs from the exact
-//          softmax weight by at most 2^-9 relative). The V tile goes through
+//          k-slot 8g+e -> token 4g+e, 8g+4+e -> token 16+4g+e. P enters as
+//          two bf16 parts, P = P_hi + P_lo (P_hi = bf16(P); P_lo = bf16 of the
+//          remainder P - P_hi, which is exact in fp32), each multiplied by V
+//          on its own MFMA: the effective weight P_hi + P_lo is within 2^-18
+//          relative of the fp32 one (a single bf16 part: 2^-9), which keeps the
+//          PV product as accurate as the reference's fp32 p * V
+//          (v2_splitkv.cu:200-204) to within fp32 summation noise. The fp32
+//          sum l accumulates the same effective weights, so the weights stay
+//          normalised. The V tile goes through
 //          LDS: written row-major with a 16-byte-chunk XOR swizzle and read
 //          back with ds_read_b64_tr_b16, whose 16-lane transpose hands lane l
 //          the 4 consecutive tokens of dim l%16 that the B operand needs
@@ -212,18 +217,21 @@ __device__ __forceinline__ void mfma_scan_segment(const ScanArgs& a, const int* 
     const float alpha = exp2_fast(st.m - ms);
     st.m = mn;
 
-    // P in bf16: per 16-token group, k-slots 4g..4g+3 = tokens 4g..4g+3.
-    uint32_t pw[2 * NG];
+    // P as bf16 pairs P_hi + P_lo: per 16-token group, k-slots 4g..4g+3 =
+    // tokens 4g..4g+3.
+    uint32_t pw[2 * NG], pl[2 * NG];
     float psum = 0.f;
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg)
 #pragma unroll
       for (int e = 0; e < 4; e += 2) {
         const f32x2_t pf = {exp2_fast(s[tg][e] - ms), exp2_fast(s[tg][e + 1] - ms)};
-        const bf16x2_t pb = __builtin_convertvector(pf, bf16x2_t);
-        const uint32_t w = __builtin_bit_cast(uint32_t, pb);
+        const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf, bf16x2_t));
+        const f32x2_t rem = {pf[0] - bf16_lo(w), pf[1] - bf16_hi(w)};
+        const uint32_t wl = __builtin_bit_cast(uint32_t, __builtin_convertvector(rem, bf16x2_t));
         pw[2 * tg + e / 2] = w;
-        psum += bf16_lo(w) + bf16_hi(w);
+        pl[2 * tg + e / 2] = wl;
+        psum += (bf16_lo(w) + bf16_lo(wl)) + (bf16_hi(w) + bf16_hi(wl));
       }
     st.lsum = fmaf(st.lsum, alpha, psum);
 
@@ -241,25 +249,43 @@ __device__ __forceinline__ void mfma_scan_segment(const ScanArgs& a, const int* 
     wave_lds_sync();
     // PV: B operand of dim block nb = V[tokens of k-slots][dim 16nb + j], read
     // transposed: lane x supplies row 4g + x/4 (+16 per token group).
+    // The P_hi products of all 8 dim blocks come first, then the P_lo ones, so
+    // no MFMA waits for the one before it.
     const int rr = 4 * g + (j >> 2);
+    if constexpr (NG == 1) {
+      // K = 16 tokens: A = P (lane: head j, tokens 4g..4g+3), B = V (dim j).
+      bf16x4_t vb[8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const int cc = 2 * nb + ((j & 3) >> 1);
-      const uint32_t half = 8u * (j & 1);
-      const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-          (lds_bf16x4_t*)(vbuf + vlds_offset(rr, cc) + half));
-      if constexpr (NG == 1) {
-        // K = 16 tokens: A = P (lane: head j, tokens 4g..4g+3), B = V (dim j).
+      for (int nb = 0; nb < 8; ++nb) {
+        const int cc = 2 * nb + ((j & 3) >> 1);
+        vb[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)(vbuf + vlds_offset(rr, cc) + 8u * (j & 1)));
         st.o[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-            __builtin_bit_cast(bf16x4_t, make_uint2(pw[0], pw[1])), v0, st.o[nb], 0, 0, 0);
-      } else {
-        // K = 32 tokens, k-slot 8g+e -> token 4g+e, 8g+4+e -> token 16+4g+e.
+            __builtin_bit_cast(bf16x4_t, make_uint2(pw[0], pw[1])), vb[nb], st.o[nb], 0, 0, 0);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        st.o[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            __builtin_bit_cast(bf16x4_t, make_uint2(pl[0], pl[1])), vb[nb], st.o[nb], 0, 0, 0);
+    } else {
+      // K = 32 tokens, k-slot 8g+e -> token 4g+e, 8g+4+e -> token 16+4g+e.
+      bf16x8_t vb[8];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const int cc = 2 * nb + ((j & 3) >> 1);
+        const uint32_t half = 8u * (j & 1);
+        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)(vbuf + vlds_offset(rr, cc) + half));
         const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
             (lds_bf16x4_t*)(vbuf + vlds_offset(rr + 16, cc) + half));
-        const bf16x8_t vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        const bf16x8_t pa = as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        st.o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, st.o[nb], 0, 0, 0);
+        vb[nb] = bf16x8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        st.o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(make_uint4(pw[0], pw[1], pw[2], pw[3])), vb[nb], st.o[nb], 0, 0, 0);
       }
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        st.o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(make_uint4(pl[0], pl[1], pl[2], pl[3])), vb[nb], st.o[nb], 0, 0, 0);
     }
     wave_lds_sync();
   };

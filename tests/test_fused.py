@@ -19,6 +19,7 @@ import pytest
 import torch
 
 import capi
+from cases import make_case
 from gpu_util import assert_close, numpy_oracle
 from test_gqa_decode import ATOL, CASES, RTOL, SCALE, alloc_ws, ref_case, stream_ptr
 
@@ -184,3 +185,33 @@ def test_fused_config3_full_size(gpu):
     assert ns > 1
     print(f"fused c3 ns={ns}", flush=True)
     check_fused(case, ns, "c3")
+
+
+def test_fused_stress_random_shapes(gpu):
+    """Bounded stress of the arrival protocol: 40 seeded random shapes
+    (kv-heads 1-16, groups 1-16, both scans and both matrix-core layouts,
+    block sizes on and off the tile, 2-64 splits, up to 48 ragged requests),
+    each launched three times back to back on one workspace, every output
+    bitwise equal to partial + merge; stops at the first mismatch."""
+    rng = np.random.default_rng(2024)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for i in range(40):
+        Hkv = int(rng.choice([1, 2, 4, 8, 16]))
+        G = int(rng.integers(1, 17))
+        B = int(rng.integers(1, 49))
+        bs = int(rng.choice([1, 7, 16, 64]))
+        ns = int(rng.integers(2, 65))
+        if i % 4 == 0 and Hkv in (4, 8) and G >= 5:
+            ns = max(ns, -(-(24 * cus) // (4 * B * Hkv)))  # the slot-group layout's grid
+        S = rng.integers(1, 4097, size=B).tolist()
+        label = f"stress {i}: Hq={G * Hkv} Hkv={Hkv} B={B} bs={bs} ns={ns}"
+        print(label, flush=True)
+        case = make_case(S, G * Hkv, Hkv, bs, pool_factor=1.2, seed=i, qkv_std=0.5)
+        want = two_launch(case, ns)
+        ws, n = fused_workspace(B, G * Hkv, ns, case[0].device, fill=float("nan"))
+        outs = [fused(case, ns, ws, n) for _ in range(3)]
+        torch.cuda.synchronize()
+        for r, out in enumerate(outs):
+            assert torch.equal(out, want), f"{label}: launch {r} differs from partial + merge"
+        assert not counters(ws, B, G * Hkv).any(), f"{label}: counters not left at zero"
+        del case, ws, outs

@@ -143,10 +143,11 @@ def stream_ptr():
     return torch.cuda.current_stream().cuda_stream
 
 
-# The matrix-core scan rounds the softmax weights to bf16 before the PV product
-# (and sums the same rounded weights into l), so a state's l and acc may differ
-# from the exact ones by up to 2^-9 relative per weight.
-W_REL = 2.5e-3
+# Relative error allowed per softmax weight in a state's l and acc: fp32
+# scores and exponentials (~1e-6), the matrix-core scan's two-part bf16 weights
+# (P_hi + P_lo, within 2^-18 of the fp32 weight) and fp32 summation over a
+# segment. A single bf16 part per weight (2^-9) would exceed it.
+W_REL = 1e-4
 
 
 @pytest.mark.parametrize("ns", [1, 4, 9])
