@@ -94,14 +94,18 @@ def make_baseline(name, case, scale):
     raise ValueError(f"unknown baseline {name!r}")
 
 
-def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
+def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus, warmup=None, runs=None):
+    """One cell's record. warmup/runs override the reference's counts (for
+    quick checks of the harness; the archived matrix uses the defaults)."""
     scale = 1.0 / math.sqrt(cases.D)
     case = cases.make_case([S] * B, Hq, Hkv, bs, pool_factor=POOL_FACTOR, seed=0, qkv_std=0.5)
     kvb = cases.kv_bytes([S] * B, Hkv)
     sol_ms = cases.sol_us(kvb) / 1e3
     checks = {"v1": cases.spot_check(KERNELS["v1"], case, scale, label="v1")}
 
-    warmup, runs = (10, 30) if (S == 32768 and B >= 32) else (10, 50)
+    dw, dr = (10, 30) if (S == 32768 and B >= 32) else (10, 50)
+    warmup = dw if warmup is None else warmup
+    runs = dr if runs is None else runs
     mb = case[3].shape[1]
     choice = ("balanced" if prefer_balanced(B, Hq, Hkv, bs, mb, num_cus)
               else num_splits_heuristic(B, Hq, Hkv, bs, mb, num_cus))
@@ -158,23 +162,29 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus):
 
 
 def write_summary(out_dir):
+    """matrix_summary.csv from every cell file: the reference's columns
+    (headtype .. pct_of_sol, then the speed ratio against the cell's baseline,
+    named after it as the reference's ratio_vs_flashinfer is), plus `choice`,
+    the automatic launch's recorded choice."""
     rows = []
     for fname in sorted(os.listdir(out_dir)):
         if not (fname.startswith("cell_") and fname.endswith(".json")):
             continue
         with open(os.path.join(out_dir, fname)) as f:
             cell = json.load(f)
-        base = cell["results"].get(cell.get("baseline", ""), {}).get("median_ms")
+        baseline = cell.get("baseline", "none")
+        base = cell["results"].get(baseline, {}).get("median_ms")
         for kernel, r in cell["results"].items():
             rows.append({
                 "headtype": f"{cell['Hq']}x{cell['Hkv']}",
                 "S": cell["S"], "B": cell["B"], "block": cell["block"],
                 "kernel": kernel,
-                "num_splits": r.get("best_splits", r.get("choice", "")),
+                "best_splits": r.get("best_splits", ""),
                 "median_ms": r["median_ms"],
                 "pct_of_sol": r["pct_of_sol"],
                 # > 1: faster than the baseline
-                "ratio_vs_baseline": base / r["median_ms"] if base else "",
+                f"ratio_vs_{baseline}": base / r["median_ms"] if base else "",
+                "choice": r.get("choice", ""),
             })
     if not rows:
         return
@@ -193,6 +203,11 @@ def main(argv=None):
     ap.add_argument("--baseline", default="sdpa", choices=["sdpa", "none"])
     ap.add_argument("--only", default=None,
                     help="comma-separated substrings; run only cells whose name contains one")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="warmup calls per variant (default: the reference's 10)")
+    ap.add_argument("--runs", type=int, default=None,
+                    help="timed calls per variant (default: the reference's 50, 30 for "
+                         "S=32768 with B>=32)")
     args = ap.parse_args(argv)
 
     out_dir = args.out_dir or os.path.join(_HERE, "results",
@@ -216,7 +231,7 @@ def main(argv=None):
             continue
         print(f"[{i}/{len(cells)}] {name}: running", flush=True)
         t0 = time.time()
-        cell = run_cell(*c, args.baseline, num_cus)
+        cell = run_cell(*c, args.baseline, num_cus, warmup=args.warmup, runs=args.runs)
         with open(path, "w") as f:
             json.dump(cell, f, indent=2)
         torch.cuda.empty_cache()
