@@ -71,7 +71,8 @@ def parse_args(argv=None):
     ap.add_argument("--sweep", action="store_true", help="also time v2 over a num_splits sweep")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
-                    help="oracle threads (default: min(16, cpu count))")
+                    help="oracle threads (default: OMP_NUM_THREADS, else the CPUs this process "
+                         "may use)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--ramp-seconds", type=float, default=0.5,
                     help="untimed steps before the warmup steps, to reach steady clocks")
@@ -448,6 +449,25 @@ def main_mla(args, dev, props):
     return 0
 
 
+def cpu_threads(args):
+    """(threads, source) for the CPU baseline: --cpu-threads if given, else this
+    process's CPU share -- OMP_NUM_THREADS where the host sets it (the GPU
+    boxes set it to their per-GPU share, 16, whatever os.cpu_count() reports),
+    capped at the CPUs the process may run on."""
+    avail = len(os.sched_getaffinity(0))
+    if args.cpu_threads:
+        return args.cpu_threads, "--cpu-threads"
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        return min(int(omp), avail), "OMP_NUM_THREADS"
+    return avail, "sched_getaffinity"
+
+
+def host_cpu_record(threads, source):
+    return {"cores": threads, "threads_from": source, "host_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
     """The MLA oracle (oracle/mla_decode_oracle.c) on this host's cores over
     whole requests of the workload (~10 s), scaled to one full step; its output
@@ -458,7 +478,7 @@ def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
     sys.path.insert(0, REPO_ROOT)
     from oracle import c_oracle  # noqa: E402  (the checker, timed as the CPU baseline)
 
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads, source = cpu_threads(args)
     B = len(S_list)
     t0 = time.perf_counter()
     c_oracle.mla_decode_ref(*mla_host_case(case, [0]), scale, causal=args.causal,
@@ -490,7 +510,8 @@ def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
         f"{'ok' if ok else 'FAILED'}")
     if not ok:
         raise SystemExit("spot check of the GPU output against the oracle failed")
-    return {"value": round(cpu_us, 1), "unit": "us", "cores": threads, "kind": "port",
+    return {"value": round(cpu_us, 1), "unit": "us", **host_cpu_record(threads, source),
+            "kind": "port",
             "sample": f"requests {sample[0]}..{sample[-1]} ({len(sample)} of {B}, "
                       f"{tokens} tokens = {frac * 100:.1f}% of the step), median of 3 runs of "
                       f"oracle/mla_decode_oracle.c, scaled to the full step",
@@ -507,7 +528,7 @@ def cpu_baseline(args, case, out, S_list, scale, gpu_us):
     sys.path.insert(0, REPO_ROOT)
     from oracle import c_oracle  # noqa: E402  (the checker, timed as the CPU baseline)
 
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    threads, source = cpu_threads(args)
     B = len(S_list)
     # Grow the sample one request at a time until it holds ~1/8 of the step or
     # the estimated run time passes ~10 s; first time one request to calibrate.
@@ -539,7 +560,8 @@ def cpu_baseline(args, case, out, S_list, scale, gpu_us):
         f"{'ok' if ok else 'FAILED'}")
     if not ok:
         raise SystemExit("spot check of the GPU output against the oracle failed")
-    return {"value": round(cpu_us, 1), "unit": "us", "cores": threads, "kind": "port",
+    return {"value": round(cpu_us, 1), "unit": "us", **host_cpu_record(threads, source),
+            "kind": "port",
             "sample": f"requests {sample[0]}..{sample[-1]} ({len(sample)} of {B}, "
                       f"{tokens} tokens = {frac * 100:.1f}% of the step), median of 3 runs of "
                       f"oracle/gqa_decode_oracle.c, scaled to the full step",

@@ -80,7 +80,15 @@ GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cac
  * same inputs, split count and device. Workspace layout (the reference's, v2_splitkv.cu:10-12):
  *   ws_acc [B, Hq, num_splits, 128] fp32, ws_m / ws_l [B, Hq, num_splits] fp32
  * ws_m holds the segment's max of scale*<q,k> (natural-log units), ws_l the sum
- * of exp(score - ws_m), ws_acc the exp-weighted sum of V rows. An empty segment
+ * of exp(score - ws_m), ws_acc the exp-weighted sum of V rows.
+ * Split rule: split i of request b covers tokens [i*chunk, min(S_b, (i+1)*chunk))
+ * with chunk = ceil(S_b / num_splits) rounded UP to a multiple of 32 tokens.
+ * The reference uses chunk = ceil(S_b / num_splits) unrounded
+ * (v2_splitkv.cu:30-32): the rounding keeps each 16-token tile inside one
+ * cache block, so for short sequences the trailing splits can be empty
+ * (S = 100, num_splits = 8: chunk 32, splits 0-3 live, 4-7 empty; the
+ * reference's chunk would be 13 with all 8 live). A caller that produces or
+ * consumes per-split states itself must use this rule. An empty segment
  * stores (-inf, 0, 0). num_splits must be in [1, GQA_DECODE_MAX_SPLITS];
  * num_splits == 1 gives output bitwise equal to gqa_decode_v1_launch.
  * Replaces gqa_decode_v2_launch (include/gqa_decode.h:18-23). */
@@ -95,7 +103,9 @@ GQA_DECODE_API int gqa_decode_v2_launch(const uint16_t* q, const uint16_t* k_cac
  * split states themselves (e.g. a context-parallel decode that all-gathers
  * partial states across devices and then merges them). Same arguments and
  * workspace contract as gqa_decode_v2_launch; _partial writes only the
- * workspace, _merge reads only the workspace. Reference counterparts: the
+ * workspace, _merge reads only the workspace (any num_splits states per
+ * (b, q-head), in whatever token split the caller chose, fold correctly; the
+ * partial kernel's own split is the 32-token-rounded rule above). Reference counterparts: the
  * partial and merge launches inside gqa_decode_v2_launch
  * (kernels/gqa_decode/v2_splitkv.cu:115-124). */
 GQA_DECODE_API int gqa_decode_v2_partial_launch(const uint16_t* q, const uint16_t* k_cache,
