@@ -229,6 +229,32 @@ GQA_DECODE_API int gqa_decode_balanced_merge_launch(
     float scale, int num_workgroups, float* workspace, size_t workspace_bytes,
     hipStream_t stream);
 
+/* Size of the device array gqa_decode_balanced_launch_noalloc uses as its
+ * workspace: 32 MiB per device (two fp32 states of all q-heads per workgroup:
+ * up to 64 q-heads at 256 workgroups). */
+#define GQA_DECODE_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* gqa_decode_balanced_launch without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No reference counterpart: the
+ * reference's launchers take caller-owned buffers and have no such variant.
+ * Its workspace is a file-scope device array of
+ * GQA_DECODE_NOALLOC_SCRATCH_BYTES in the library, one copy per device
+ * (resolved for the stream's device on the first call there, and held until
+ * the process ends); the call allocates nothing. Same arguments, kernels and
+ * bits as gqa_decode_balanced_launch with the same num_workgroups. Returns
+ * hipErrorOutOfMemory, launching nothing, when
+ * gqa_decode_balanced_workspace_bytes(B, Hq, Hkv, num_workgroups) exceeds
+ * GQA_DECODE_NOALLOC_SCRATCH_BYTES; otherwise as gqa_decode_balanced_launch.
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device (different streams without ordering, or threads) race and give
+ * wrong results; calls in one stream's order do not. The array needs no
+ * clearing: every byte a launch reads, it wrote. */
+GQA_DECODE_API int gqa_decode_balanced_launch_noalloc(
+    const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
+    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+    float scale, int num_workgroups, hipStream_t stream);
+
 /* 1 if gqa_decode_balanced_launch is expected to beat the split-KV launch with
  * gqa_decode_pick_num_splits' count for this shape on num_cus CUs (<= 0: the
  * current device), else 0 (also for shapes the balanced launcher does not

@@ -36,6 +36,7 @@
 #include "gqa_scan_valu.hpp"
 #include "gqa_decode.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace gqa {
@@ -636,6 +637,65 @@ extern "C" int gqa_decode_balanced_merge_launch(
   return balanced_launch(BalancedPart::kMerge, q, k_cache, v_cache, block_table, seq_lens, out, B,
                          Hq, Hkv, block_size, max_blocks, scale, num_workgroups, workspace,
                          workspace_bytes, stream);
+}
+
+// The allocation-free launch's workspace: a file-scope device array, one copy
+// per device at that device's own address. In host code `scratch` names a
+// host-side stand-in, never the device memory: kernels get the address that
+// hipGetSymbolAddress returns for the device, looked up once per device with
+// that device current and kept here.
+static __device__ __align__(256) uint8_t scratch[GQA_DECODE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current
+// device for the null stream).
+hipError_t scratch_for_stream(hipStream_t stream, void** ptr) {
+  int cur = 0, dev = 0;
+  hipError_t err = hipGetDevice(&cur);
+  if (err != hipSuccess) return err;
+  dev = cur;
+  if (stream != nullptr && (err = hipStreamGetDevice(stream, &dev)) != hipSuccess) return err;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (err = hipSetDevice(dev)) != hipSuccess) return err;
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (err == hipSuccess) err = back;
+    }
+    if (err != hipSuccess) return err;
+    if (p == nullptr || ((uintptr_t)p & 255) != 0) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int gqa_decode_balanced_launch_noalloc(
+    const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
+    const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
+    float scale, int num_workgroups, hipStream_t stream) {
+  const size_t need = gqa_decode_balanced_workspace_bytes(B, Hq, Hkv, num_workgroups);
+  if (need == 0)  // B == 0 (nothing to do) or arguments the launcher rejects
+    return balanced_launch(BalancedPart::kBoth, q, k_cache, v_cache, block_table, seq_lens, out,
+                           B, Hq, Hkv, block_size, max_blocks, scale, num_workgroups, nullptr, 0,
+                           stream);
+  if (need > GQA_DECODE_NOALLOC_SCRATCH_BYTES) return hipErrorOutOfMemory;
+  void* ws = nullptr;
+  const hipError_t err = scratch_for_stream(stream, &ws);
+  if (err != hipSuccess) return err;
+  return balanced_launch(BalancedPart::kBoth, q, k_cache, v_cache, block_table, seq_lens, out, B,
+                         Hq, Hkv, block_size, max_blocks, scale, num_workgroups,
+                         static_cast<float*>(ws), GQA_DECODE_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size, int max_blocks,

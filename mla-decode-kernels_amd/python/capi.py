@@ -75,6 +75,8 @@ def lib():
             fn = getattr(L, name)
             fn.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
             fn.restype = _i
+        L.gqa_decode_balanced_launch_noalloc.argtypes = _LAUNCH_ARGS + [_i, _vp]
+        L.gqa_decode_balanced_launch_noalloc.restype = _i
         L.gqa_decode_prefer_balanced.argtypes = [_i, _i, _i, _i, _i, _i]
         L.gqa_decode_prefer_balanced.restype = _i
         for fn in (L.mla_decode_launch, L.mla_decode_splitkv_launch, L.mla_decode_balanced_launch):
@@ -180,3 +182,13 @@ def mla_workspace_bytes(B, s_q, h_q, num_splits):
 
 def mla_pick_num_splits(B, s_q, h_q, block_size, max_blocks, num_cus):
     return lib().mla_decode_pick_num_splits(B, s_q, h_q, block_size, max_blocks, num_cus)
+
+
+def balanced_launch_noalloc(*args):
+    """gqa_decode_balanced_launch_noalloc: the balanced launch on the library's
+    own per-device scratch array (no workspace argument)."""
+    return lib().gqa_decode_balanced_launch_noalloc(*args)
+
+
+# GQA_DECODE_NOALLOC_SCRATCH_BYTES in include/gqa_decode.h.
+NOALLOC_SCRATCH_BYTES = 32 << 20

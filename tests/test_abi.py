@@ -28,7 +28,7 @@ def test_library_exports_every_declared_function():
         "gqa_decode_pick_num_splits",
         "gqa_decode_balanced_launch", "gqa_decode_balanced_workspace_bytes",
         "gqa_decode_balanced_partial_launch", "gqa_decode_balanced_merge_launch",
-        "gqa_decode_prefer_balanced",
+        "gqa_decode_balanced_launch_noalloc", "gqa_decode_prefer_balanced",
     ])
     lib = capi.lib()
     for name in declared:
