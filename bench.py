@@ -80,6 +80,14 @@ def parse_args(argv=None):
                     help="instead: time a plain device copy of MIB MiB (torch.neg into a second "
                          "buffer), the known-size kernel that calibrates rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--lib", default=None, metavar="PATH",
+                    help="C ABI library the timed launches use (default: the in-tree "
+                         "lib/libgqa_decode_hip.so); for profiling a build.py --variant build. "
+                         "The torch op, which links the in-tree library, is then not timed")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="instead: the streaming-read ceiling of config 2's cache (1 GiB of K+V) "
+                         "in the scans' head-strided gather and in whole-slot reads, with "
+                         "non-temporal and plain loads (lib/libgqa_stream_probe.so)")
     return ap.parse_args(argv)
 
 
@@ -125,11 +133,16 @@ def main(argv=None):
     import cases
     from binding import KERNELS, gqa_decode_balanced, gqa_decode_v2
 
+    if args.lib:
+        capi.LIB_PATH = os.path.abspath(args.lib)
+        log(f"C ABI library: {capi.LIB_PATH}")
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda", 0)
     props = torch.cuda.get_device_properties(dev)
+    if args.stream_probe:
+        return stream_probe(torch, cases, dev)
     if args.copy_probe:
         n = args.copy_probe << 20
         x = torch.ones(n // 4, dtype=torch.float32, device=dev)
@@ -250,20 +263,23 @@ def main(argv=None):
         f"dominant kernel avg {kern_avg_us:.2f} us ({kvb / kern_avg_us / 1e3:.1f} GB/s), "
         f"wall {wall / K * 1e3:.3f} ms/step")
 
-    # The torch operator, timed the reference's way.
-    if args.kernel == "balanced":
-        op = lambda: gqa_decode_balanced(*case, scale)  # noqa: E731
-    elif args.kernel == "v2":
-        op = lambda: gqa_decode_v2(*case, scale, num_splits=args.num_splits if balanced else ns)  # noqa: E731
-    else:
-        op = lambda: KERNELS[args.kernel](*case, scale)  # noqa: E731
-    op_ms = cases.time_op(op, warmup=3, runs=min(K, 30))
-    out_op = op()
-    torch.cuda.synchronize()
-    assert torch.equal(out_op, out), "torch op and C ABI outputs differ"
+    # The torch operator, timed the reference's way (not for a --lib variant:
+    # the op runs the in-tree library).
+    op_ms = None
+    if not args.lib:
+        if args.kernel == "balanced":
+            op = lambda: gqa_decode_balanced(*case, scale)  # noqa: E731
+        elif args.kernel == "v2":
+            op = lambda: gqa_decode_v2(*case, scale, num_splits=args.num_splits if balanced else ns)  # noqa: E731
+        else:
+            op = lambda: KERNELS[args.kernel](*case, scale)  # noqa: E731
+        op_ms = cases.time_op(op, warmup=3, runs=min(K, 30))
+        out_op = op()
+        torch.cuda.synchronize()
+        assert torch.equal(out_op, out), "torch op and C ABI outputs differ"
 
     sweep = None
-    if args.sweep and args.kernel == "v2":
+    if args.sweep and args.kernel == "v2" and not args.lib:
         sweep = {}
         for s in [1, 2, 4, 8, 16, 32, 64, 128]:
             ms = cases.time_op(lambda: gqa_decode_v2(*case, scale, num_splits=s), 3, 20)
@@ -287,7 +303,9 @@ def main(argv=None):
         "dtype": "bf16",
         "accum": "fp32",
         "data": f"synthetic N(0,1) bf16, seed {args.seed}",
-        "config": {"workload": f"{args.config}: {cfg['desc']}", "Hq": Hq, "Hkv": Hkv, "B": B,
+        "config": {"workload": f"{args.config}: {cfg['desc']}" + (
+                       f" [library {os.path.relpath(capi.LIB_PATH, REPO_ROOT)}]" if args.lib else ""),
+                   "Hq": Hq, "Hkv": Hkv, "B": B,
                    "S": cfg["S"] if cfg["S"] else "U[1,32768]", "block": bs,
                    "kernel": args.kernel,
                    "num_splits": split_label if args.kernel in ("v2", "balanced") else None},
@@ -295,7 +313,7 @@ def main(argv=None):
         "achieved_gbps": round(kvb / median_us / 1e3, 1),
         "kv_bytes": kvb,
         "sol_us": round(sol, 3),
-        "op_median_us": round(op_ms * 1e3, 3),
+        "op_median_us": round(op_ms * 1e3, 3) if op_ms is not None else None,
         "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv, balanced, Hkv),
                      "achieved": round(achieved, 1),
                      "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
@@ -446,6 +464,52 @@ def main_mla(args, dev, props):
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_mla(args, case, out, lse, S_list, scale, median_us)
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def stream_probe(torch, cases, dev):
+    """Read rate of config 2's K and V (32 requests x 8192 token slots x 8
+    kv-heads x 256 B each: 1 GiB together), every byte once, no arithmetic:
+    the scans' head-strided gather (one workgroup of 4 waves per (kv-head,
+    request), as the VALU scan runs config 2 at one split), whole-slot reads
+    (4 waves per (request, split), 8 splits) and a plain linear read of both
+    buffers (256 workgroups of 4 waves), each with non-temporal and plain
+    loads. Events around each launch, median of 20 after 5 warmup launches."""
+    import ctypes
+
+    path = os.path.join(PKG_DIR, "lib", "libgqa_stream_probe.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} missing: run `python mla-decode-kernels_amd/build.py`")
+    L = ctypes.CDLL(path)
+    L.gqa_stream_probe_launch.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 5 + [
+        ctypes.c_void_p]
+    L.gqa_stream_probe_launch.restype = ctypes.c_int
+    requests, slots, splits = 32, 8192, 8
+    nbytes = requests * slots * 2048
+    k = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    v = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    k.random_(0, 256)
+    v.random_(0, 256)
+    sink = torch.empty(requests * 8 * 256, dtype=torch.int32, device=dev)
+    sp = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for pattern, pname, nsplit in ((0, "head_strided", 1), (1, "whole_slot", splits),
+                                   (2, "linear", 256)):
+        for nt in (1, 0):
+            def launch():
+                rc = L.gqa_stream_probe_launch(k.data_ptr(), v.data_ptr(), sink.data_ptr(),
+                                               pattern, requests, slots, nsplit, nt, sp)
+                if rc != 0:
+                    raise RuntimeError(f"gqa_stream_probe_launch returned {rc}")
+            ms = cases.time_op(launch, warmup=5, runs=20)
+            key = f"{pname}_{'nt' if nt else 'plain'}"
+            res[key] = {"median_us": round(ms * 1e3, 2),
+                        "tbps": round(2 * nbytes / ms / 1e9, 3),
+                        "frac_of_8tbps": round(2 * nbytes / ms / 1e9 / 8.0, 4)}
+            log(f"stream probe {key}: {ms * 1e3:.2f} us, {2 * nbytes / ms / 1e9:.3f} TB/s")
+    print(json.dumps({"stream_probe": "config 2 cache, 1 GiB K+V, identity block table",
+                      "bytes": 2 * nbytes, "results": res, "clocks": cases.gpu_clocks()}),
+          flush=True)
     return 0
 
 

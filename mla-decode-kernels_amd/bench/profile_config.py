@@ -18,9 +18,26 @@ Passes (each counter set within one rocprofv3 pass's hardware limits):
   lds     SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS SQ_WAVES SQ_INSTS_VMEM_RD
           GRBM_GUI_ACTIVE
   l2      TCC_HIT_sum TCC_MISS_sum
+  stall   SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU
+          SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_SCA SQ_ACTIVE_INST_MISC
   copy_fetch / copy_write   the copy calibration (FETCH_SIZE / WRITE_SIZE)
 This script never touches the GPU itself: rocprofv3 starts bench.py as its
-program (after `--`), one child process per pass.
+program (after `--`), one child process per pass. --bench-args adds bench.py
+arguments to every pass but the copies (e.g. "--num-splits 4", or "--lib
+<path>" to profile a library built with build.py --variant).
+
+The summary also gives, per kernel, the counterparts of the reference
+extractor's stall and occupancy sections (analysis/ncu/extract.py:126-191):
+  wave-cycle breakdown  the stall pass's counters as fractions of
+      SQ_WAVE_CYCLES (all in quad-cycles): waiting on a dependency
+      (SQ_WAIT_ANY: s_waitcnt on memory, LDS or a previous result), waiting
+      for issue (SQ_WAIT_INST_ANY: ready, but the SIMD issued another wave's
+      instruction or the unit was busy), and issuing each instruction type
+      (SQ_ACTIVE_INST_*); the three largest are listed as the top reasons;
+  occupancy limiter     waves per SIMD allowed by each resource of the
+      dispatch (VGPRs + AGPRs per lane out of 512 in granules of 8, LDS per
+      workgroup out of 160 KiB, 8 waves per SIMD, and the grid itself),
+      from the kernel-trace columns; the smallest is the limiter.
 """
 
 import argparse
@@ -48,31 +65,34 @@ PASSES = {
     "lds": ["--pmc", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_WAVES",
             "SQ_INSTS_VMEM_RD", "GRBM_GUI_ACTIVE"],
     "l2": ["--pmc", "TCC_HIT_sum", "TCC_MISS_sum"],
+    "stall": ["--pmc", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VALU",
+              "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_SCA",
+              "SQ_ACTIVE_INST_MISC"],
     "copy_fetch": ["--pmc", "FETCH_SIZE"],
     "copy_write": ["--pmc", "WRITE_SIZE"],
 }
 SHORT_RUN = ["--steps", "3", "--warmup", "1", "--ramp-seconds", "0", "--no-cpu-baseline"]
 
 
-def bench_args(pass_name, config):
+def bench_args(pass_name, config, extra=()):
     if pass_name.startswith("copy_"):
         return ["--copy-probe", "1024"]
     if pass_name == "trace":
-        return ["--config", config, "--steps", "50", "--no-cpu-baseline"]
-    return ["--config", config] + SHORT_RUN
+        return ["--config", config, "--steps", "50", "--no-cpu-baseline"] + list(extra)
+    return ["--config", config] + SHORT_RUN + list(extra)
 
 
-def command(pass_name, config, out_dir):
+def command(pass_name, config, out_dir, extra=()):
     return (["rocprofv3", "-f", "csv"] + PASSES[pass_name] +
             ["-d", os.path.join(out_dir, pass_name), "-o", "run", "--", sys.executable, BENCH] +
-            bench_args(pass_name, config))
+            bench_args(pass_name, config, extra))
 
 
-def run_passes(config, out_dir, passes, timeout):
+def run_passes(config, out_dir, passes, timeout, extra=()):
     os.makedirs(out_dir, exist_ok=True)
     env = dict(os.environ, TMPDIR="/tmp")
     for name in passes:
-        cmd = command(name, config, out_dir)
+        cmd = command(name, config, out_dir, extra)
         print("==", name, " ".join(cmd), flush=True)
         with open(os.path.join(out_dir, f"{name}.log"), "w") as log:
             # A pass that asks for more counters than the hardware holds hangs
@@ -127,6 +147,56 @@ def counter_means(directory, pattern="gqa|mla|neg_kernel"):
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
+STALL_PARTS = [("dependency wait", "SQ_WAIT_ANY"), ("issue wait", "SQ_WAIT_INST_ANY"),
+               ("VALU/MFMA issue", "SQ_ACTIVE_INST_VALU"), ("VMEM issue", "SQ_ACTIVE_INST_VMEM"),
+               ("LDS issue", "SQ_ACTIVE_INST_LDS"), ("scalar issue", "SQ_ACTIVE_INST_SCA"),
+               ("branch/message", "SQ_ACTIVE_INST_MISC")]
+
+
+def stall_breakdown(counters, kernel):
+    """[(label, fraction of SQ_WAVE_CYCLES)] for one kernel, largest first, or
+    None without the stall pass."""
+    total = counters.get((kernel, "SQ_WAVE_CYCLES"))
+    if not total:
+        return None
+    parts = [(label, counters[(kernel, c)] / total) for label, c in STALL_PARTS
+             if (kernel, c) in counters]
+    return sorted(parts, key=lambda p: -p[1])
+
+
+LDS_BYTES_PER_CU = 160 * 1024
+VGPRS_PER_SIMD_LANE = 512
+MAX_WAVES_PER_SIMD = 8
+
+
+def occupancy(row, num_cus=256):
+    """({resource: waves per SIMD it allows}, limiter) for one kernel-trace row."""
+    wg = int(row["Workgroup_Size_X"]) * int(row["Workgroup_Size_Y"]) * int(row["Workgroup_Size_Z"])
+    waves_per_wg = -(-wg // 64)
+    vgprs = int(row.get("VGPR_Count") or 0) + int(row.get("Accum_VGPR_Count") or 0)
+    lds = int(row.get("LDS_Block_Size") or 0)
+    grid = int(row["Grid_Size_X"]) * int(row["Grid_Size_Y"]) * int(row["Grid_Size_Z"])
+    limits = {"max waves": MAX_WAVES_PER_SIMD}
+    if vgprs:
+        limits["VGPRs"] = VGPRS_PER_SIMD_LANE // (-(-vgprs // 8) * 8)
+    if lds:
+        wgs = LDS_BYTES_PER_CU // lds
+        limits["LDS"] = wgs * waves_per_wg / 4
+    limits["grid"] = grid / 64 / (num_cus * 4)
+    limiter = min(limits, key=limits.get)
+    return limits, limiter
+
+
+def occupancy_rows(directory, pattern="gqa|mla|probe"):
+    """{kernel: first kernel-trace row} (the resource columns are per kernel)."""
+    out = {}
+    for r in read_csvs(directory, "kernel_trace.csv"):
+        name = r.get("Kernel_Name", "")
+        if re.search(pattern, name) and r.get("Workgroup_Size_X"):
+            out.setdefault(short_name(name), r)
+    return out
+
+
 def calibration(root):
     """Bytes per counter unit for FETCH_SIZE and WRITE_SIZE: the copy of
     COPY_BYTES read and written, over what each counter reported for it."""
@@ -155,6 +225,32 @@ def summarize(root):
     lines += ["", "| kernel | counter | mean per dispatch |", "|---|---|---|"]
     for (k, c), v in sorted(counters.items()):
         lines.append(f"| {k} | {c} | {v:,.0f} |")
+    stall = counter_means(os.path.join(root, "stall"))
+    breakdowns = {k: stall_breakdown(stall, k) for k in sorted({k for k, _ in stall})}
+    breakdowns = {k: b for k, b in breakdowns.items() if b}
+    if breakdowns:
+        lines += ["", "Wave-cycle breakdown (fractions of SQ_WAVE_CYCLES; a wave can wait and",
+                  "issue in the same cycle, so the parts need not sum to 1):", "",
+                  "| kernel | " + " | ".join(label for label, _ in STALL_PARTS) + " | top 3 |",
+                  "|---|" + "---|" * (len(STALL_PARTS) + 1)]
+        for k, b in breakdowns.items():
+            frac = dict(b)
+            top = ", ".join(f"{label} {f:.0%}" for label, f in b[:3])
+            lines.append(f"| {k} | " + " | ".join(
+                f"{frac[label]:.3f}" if label in frac else "-" for label, _ in STALL_PARTS)
+                + f" | {top} |")
+    occ = occupancy_rows(os.path.join(root, "trace"))
+    if occ:
+        lines += ["", "Occupancy (waves per SIMD each resource allows; the smallest limits):", "",
+                  "| kernel | VGPRs+AGPRs | LDS bytes | waves/workgroup | by VGPRs | by LDS | "
+                  "by grid | limiter |", "|---|---|---|---|---|---|---|---|"]
+        for k, r in sorted(occ.items()):
+            limits, limiter = occupancy(r)
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            vg = int(r.get("VGPR_Count") or 0) + int(r.get("Accum_VGPR_Count") or 0)
+            lines.append(f"| {k} | {vg} | {r.get('LDS_Block_Size', '')} | {-(-wg // 64)} | "
+                         f"{limits.get('VGPRs', '-')} | {limits.get('LDS', '-')} | "
+                         f"{limits['grid']:.2f} | {limiter} |")
     cal = calibration(root)
     traffic = None
     if cal and dur:
@@ -192,12 +288,15 @@ def main(argv=None):
     ap.add_argument("--passes", default=",".join(PASSES))
     ap.add_argument("--timeout", type=int, default=300, help="seconds per pass")
     ap.add_argument("--summarize", default=None, help="only summarize an existing output dir")
+    ap.add_argument("--bench-args", default="",
+                    help="extra bench.py arguments for every pass but the copies")
     args = ap.parse_args(argv)
     root = args.summarize or args.out_dir
     if root is None:
         ap.error("give --out-dir (run and summarize) or --summarize <dir>")
     if not args.summarize:
-        run_passes(args.config, root, [p for p in args.passes.split(",") if p], args.timeout)
+        run_passes(args.config, root, [p for p in args.passes.split(",") if p], args.timeout,
+                   args.bench_args.split())
     text, traffic = summarize(root)
     with open(os.path.join(root, "summary.md"), "w") as f:
         f.write(text + "\n")

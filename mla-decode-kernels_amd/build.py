@@ -2,10 +2,15 @@
 
     python mla-decode-kernels_amd/build.py            # kernels + extension
     python mla-decode-kernels_amd/build.py --no-ext   # kernel library only
+    python mla-decode-kernels_amd/build.py --variant NAME --define MACRO=VALUE ...
+        # an experiment build of the kernel library with compile-time
+        # switches, into _build/NAME/ (git-ignored; for bench.py --lib)
 
 Products (in-tree, git-ignored, shipped with the source tree):
   lib/libgqa_decode_hip.so   hipcc --offload-arch=gfx950: every kernel + the C ABI
   lib/gqa_decode_ext*.so     g++: host-only torch operator layer linking the above
+  lib/libgqa_stream_probe.so hipcc: the streaming-read probe bench.py measures
+                             the bandwidth ceiling with (not on the decode path)
 
 The extension is compiled as plain C++ (no .cu/.hip source, so torch's
 hipify pass never runs); it reaches the GPU only through the C ABI.
@@ -28,6 +33,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 KERNEL_LIB = os.path.join(LIB_DIR, "libgqa_decode_hip.so")
+PROBE_LIB = os.path.join(LIB_DIR, "libgqa_stream_probe.so")
 HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip", "gqa_decode_mfma.hip",
                "gqa_decode_balanced.hip", "mla_decode.hip"]
 # Packed fp32 VALU ops are disabled for all device code.
@@ -52,16 +58,25 @@ def _run(cmd, cwd=None):
     return time.time() - t0
 
 
-def build_kernels():
-    os.makedirs(LIB_DIR, exist_ok=True)
+def build_kernels(out=KERNEL_LIB, defines=()):
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    tmp = KERNEL_LIB + ".tmp"
-    extra = os.environ.get("GQA_HIPCC_FLAGS", "").split()  # experiments only
-    dt = _run([hipcc, *HIP_FLAGS, *extra, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
-    os.replace(tmp, KERNEL_LIB)
-    print(f"built {os.path.relpath(KERNEL_LIB, REPO_ROOT)} in {dt:.1f}s")
-    return KERNEL_LIB
+    tmp = out + ".tmp"
+    flags = [f"-D{d}" for d in defines]
+    dt = _run([hipcc, *HIP_FLAGS, *flags, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    os.replace(tmp, out)
+    print(f"built {os.path.relpath(out, REPO_ROOT)} in {dt:.1f}s")
+    return out
+
+
+def build_probe():
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    tmp = PROBE_LIB + ".tmp"
+    dt = _run([hipcc, *HIP_FLAGS, "-shared", os.path.join(CSRC, "stream_probe.hip"), "-o", tmp])
+    os.replace(tmp, PROBE_LIB)
+    print(f"built {os.path.relpath(PROBE_LIB, REPO_ROOT)} in {dt:.1f}s")
+    return PROBE_LIB
 
 
 def ext_filename():
@@ -101,10 +116,21 @@ def build_extension():
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--no-ext", action="store_true", help="build the kernel library only")
+    ap.add_argument("--variant", default=None,
+                    help="build only the kernel library, into _build/VARIANT/")
+    ap.add_argument("--define", action="append", default=[], metavar="MACRO[=VALUE]",
+                    help="compile-time switch for a --variant build (e.g. GQA_MFMA_MIN_GROUP=17)")
     args = ap.parse_args(argv)
     if shutil.which(os.path.join(ROCM, "bin", "hipcc")) is None:
         sys.exit(f"hipcc not found under {ROCM}")
+    if args.define and not args.variant:
+        ap.error("--define needs --variant (the in-tree library is built as shipped)")
+    if args.variant:
+        build_kernels(os.path.join(PKG_DIR, "_build", args.variant, "libgqa_decode_hip.so"),
+                      args.define)
+        return
     build_kernels()
+    build_probe()
     if not args.no_ext:
         build_extension()
 

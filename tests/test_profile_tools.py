@@ -79,3 +79,29 @@ def test_short_name_drops_signature_and_anonymous_namespace():
                          "true>(gqa::ScanArgs)") == "gqa::gqa_decode_mfma_kernel<8, 16, true, true>"
     assert pc.short_name("gqa::gqa_decode_merge_kernel(float const*, int)") == \
         "gqa::gqa_decode_merge_kernel"
+
+
+def test_stall_breakdown_and_occupancy(tmp_path):
+    root = str(tmp_path)
+    k = "void gqa::(anonymous namespace)::gqa_decode_scan_kernel<4, 4, true>(gqa::ScanArgs)"
+    res = dict(LDS_Block_Size=90112, VGPR_Count=96, Accum_VGPR_Count=0, SGPR_Count=48,
+               Workgroup_Size_X=256, Workgroup_Size_Y=1, Workgroup_Size_Z=1,
+               Grid_Size_X=2048, Grid_Size_Y=32, Grid_Size_Z=1)
+    write_csv(os.path.join(root, "trace", "x", "run_kernel_trace.csv"),
+              [dict(Kernel_Name=k, Start_Timestamp=0, End_Timestamp=160_000, **res)])
+    vals = {"SQ_WAVE_CYCLES": 1000, "SQ_WAIT_ANY": 700, "SQ_WAIT_INST_ANY": 100,
+            "SQ_ACTIVE_INST_VALU": 300, "SQ_ACTIVE_INST_VMEM": 50, "SQ_ACTIVE_INST_LDS": 20,
+            "SQ_ACTIVE_INST_SCA": 10, "SQ_ACTIVE_INST_MISC": 5}
+    write_csv(os.path.join(root, "stall", "x", "run_counter_collection.csv"),
+              [dict(Kernel_Name=k, Counter_Name=c, Counter_Value=v) for c, v in vals.items()])
+    b = pc.stall_breakdown(pc.counter_means(os.path.join(root, "stall")),
+                           pc.short_name(k))
+    assert [label for label, _ in b[:3]] == ["dependency wait", "VALU/MFMA issue", "issue wait"]
+    assert dict(b)["dependency wait"] == pytest.approx(0.7)
+    # 96 VGPRs -> 5 waves per SIMD; 88 KiB of LDS -> 1 workgroup of 4 waves per CU
+    # -> 1 wave per SIMD; 2048 x 32 threads = 1024 waves = 1 per SIMD on 256 CUs.
+    limits, limiter = pc.occupancy(res)
+    assert limits["VGPRs"] == 5 and limits["LDS"] == 1 and limits["grid"] == 1
+    assert limiter in ("LDS", "grid")
+    text, _ = pc.summarize(root)
+    assert "dependency wait 70%" in text and "| 96 | 90112 | 4 |" in text
