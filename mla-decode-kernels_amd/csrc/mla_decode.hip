@@ -16,16 +16,22 @@
 //                 computes the tile prefix sums on the device), walked piece
 //                 by piece; requests cut between shares are merged after.
 //
-// LDS tile layout ("A order", swizzled): 36 blocks of 1 KiB, block (tg, kk)
-// for token group tg (16 tokens) and 32-dim k-step kk; within a block the
-// 16-byte slot of token t16 and dims 8q .. 8q + 8 is 16 q + (t16 ^ 8 (q & 1)).
-// Lane (j = lane % 16, g = lane / 16) of a copy fills slot 16 g + j, so whole
-// 1 KiB blocks are written; the swizzle spreads the transposing PV reads over
-// all LDS banks.
+// LDS tile layout: 4 row blocks of 8 tokens, each 9 column blocks of 1 KiB
+// (8 rows x 128 bytes = 64 dims) plus 16 bytes, so that consecutive row
+// blocks start 16 bytes apart modulo the 256-byte bank cycle; within a column
+// block, row r sits at 128 r and its 16-byte chunk c at position
+// c ^ chunk_swz(r). Each copy instruction fills one column block: 8 lanes per
+// row read that row's 128 contiguous bytes from HBM (a copy of 16 rows x 64
+// bytes per instruction streamed at ~4.5 TB/s, 8 x 128 bytes at ~6.2 TB/s,
+// measured on MI355X), and the swizzle only permutes lanes within a row.
+// Both operand reads below are free of bank conflicts in this layout (the
+// QK ds_read_b128 phases of 16 lanes and the PV ds_read_b64_tr_b16 groups),
+// and both address as a per-lane base plus a per-step immediate.
 //
 //   QK^T   S^T[16 tok x 16 rows] = K[tok x 576] . Q^T[576 x 16 rows]: 18
-//          MFMAs per token group and row block; A from LDS (shared by both
-//          row blocks), B = Q^T in registers (lane: row j, dims 32 kk + 8 g).
+//          MFMAs per token group and row block; A from LDS (lane: token j,
+//          dims 32 kk + 8 g; shared by both row blocks), B = Q^T in registers
+//          (lane: row j, dims 32 kk + 8 g).
 //   softmax on the C layout (lane: row j, tokens 4 g + e), base 2, fp32,
 //          against a per-row reference max fixed at the row's first live
 //          tile (see kRefSlack); P rounded to bf16, l sums the rounded values.
@@ -61,7 +67,9 @@ constexpr int kWaves = 4;
 constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerGroup = kWaves * kRowsPerWave;  // 128
 constexpr int kTileBlocks = 2 * kKSteps;              // 36 blocks of 1 KiB
-constexpr int kTileBytes = kTileBlocks * 1024;
+constexpr int kColBlocks = kD / 64;                   // 9 per row block of 8 tokens
+constexpr int kRowBlockBytes = kColBlocks * 1024 + 16;
+constexpr int kTileBytes = 4 * kRowBlockBytes;
 constexpr int kStageLoads = kTileBlocks / kWaves;     // 9 per wave per tile
 // Tiles in the LDS ring: while a tile is consumed, the next kDepth - 1 are in
 // flight from HBM (about 100 KiB per CU, enough to cover the latency at this
@@ -69,6 +77,11 @@ constexpr int kStageLoads = kTileBlocks / kWaves;     // 9 per wave per tile
 constexpr int kDepth = 4;
 constexpr int kNB = kDV / 16;                         // 32 PV column blocks
 static_assert(kTileBlocks % kWaves == 0, "staging blocks must split evenly");
+static_assert(kTileBlocks == 4 * kColBlocks, "a tile is 4 row blocks of 9 column blocks");
+
+// Position XOR of row r's 16-byte chunks in a column block (a table found by
+// an exhaustive bank-conflict check of both operand reads over this layout).
+__device__ __forceinline__ int chunk_swz(int r) { return (int)((0x46226400u >> (4 * r)) & 7u); }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -193,14 +206,27 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  // LDS slot swizzle: the 16-byte slot of token t16 (within its 16-token
-  // group) and dims 8q .. 8q + 8 (within the 32-dim k-step) is
-  // 16 q + (t16 ^ 8 (q & 1)). Lane (j, g) therefore copies token j ^ 8 (g & 1)
-  // into slot 16 g + j, and reads its own QK operand (token j) from slot
-  // kslot; the transposing PV reads then hit 32 distinct bank pairs per
-  // half-wave instead of 16.
-  const int js = j ^ ((g & 1) << 3);
-  const int kslot = 16 * g + js;
+  // Copies: lane x fills row cr = x / 8 of a column block, position x % 8,
+  // from that row's chunk cc = (x % 8) ^ chunk_swz(cr).
+  const int cr = lane >> 3, cc = (lane & 7) ^ chunk_swz(lane >> 3);
+  // Tile-relative LDS offsets of this lane's operands (plus a per-step
+  // immediate): QK A operand of token group tg, k-step parity par (token
+  // 16 tg + j, chunk 4 par + g of column block kk / 2), and PV B operand of
+  // column-block quarter q = nb % 4 (tokens 4 g + j / 4 (+16), dims
+  // 16 nb + 4 (j % 4) .. +4: chunk 2 q + (j % 4) / 2, half j % 2).
+  // (Token group 1 is two row blocks on: an immediate.)
+  uint32_t qoff[2], voff4[4];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+    qoff[par] = (uint32_t)((j >> 3) * kRowBlockBytes + (j & 7) * 128 +
+                           16 * ((4 * par + g) ^ chunk_swz(j & 7)));
+  {
+    const int vr = 4 * (g & 1) + (j >> 2);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      voff4[q] = (uint32_t)((g >> 1) * kRowBlockBytes + vr * 128 +
+                            16 * ((2 * q + ((j & 3) >> 1)) ^ chunk_swz(vr)) + 8 * (j & 1));
+  }
   // Waves whose rows all lie past R compute on zero queries (their results are
   // not stored): a wave-dependent branch around the tile work would make the
   // compiler copy the accumulators on every tile.
@@ -235,91 +261,86 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const uint32_t tiles_lds = (uint32_t)(uintptr_t)(lds_u8*)&tiles[0][0];
 
-  // Staging of tile k into ring slot k % kDepth: wave w copies blocks
-  // w + 4 i (i < 9): token group tg = blk / 18, dims 32 kk + 8 g. A lane's
-  // two tokens are 16 tg + j; tokens at or past seg_end read the tile's first
-  // token instead (masked later), so nothing outside the request's live cache
-  // rows is touched. Block ids come from scalar loads, which keeps the vector
-  // memory counter for the copies alone.
+  // Staging of tile k into ring slot k % kDepth: wave w copies column blocks
+  // blk = w + 4 i (i < 9): row block rb8 = blk / 9 (tokens 8 rb8 .. +8),
+  // column block cb = blk % 9 (dims 64 cb .. +64). A lane's row is
+  // 8 rb8 + cr; tokens at or past seg_end read the tile's first token instead
+  // (masked later), so nothing outside the request's live cache rows is
+  // touched. Block ids come from scalar loads, which keeps the vector memory
+  // counter for the copies alone.
   // The refill copies of the block-uniform path are issued two per QK^T
   // k-step rather than in one burst after the barrier (a burst queues behind
   // the other waves' copies and holds the wave); Plan carries what they need,
   // and the block id is loaded one iteration ahead, before the barrier, so
   // that its scalar-load latency overlaps the wait for the landing tile.
+  // (Plan holds only wave-uniform values: a lane's source offset is its row
+  // offset, or its chunk of the tile's first token for rows past seg_end.)
   struct Plan {
     const uint16_t* base;
-    uint32_t voff[2];
+    int nvalid;
     uint32_t slot;
   };
+  const uint32_t lane_row_off = (uint32_t)(cr * kD + 8 * cc) * 2u, lane_first_off = 16u * cc;
   auto block_id = [&](int k) -> int {
     return btc[gqa::fastdiv((uint32_t)(seg_start + kTile * k), a.bs_div)];
+  };
+  // The LDS address of column block blk of the slot at `slot`.
+  auto block_lds = [&](uint32_t slot, int blk) -> uint32_t {
+    const int rb8 = blk / kColBlocks, cb = blk - rb8 * kColBlocks;
+    return slot + (uint32_t)(rb8 * kRowBlockBytes + cb * 1024);
   };
   auto prep = [&](int k, int id) -> Plan {
     const int ts = seg_start + kTile * k;
     Plan p;
     p.slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
-    int tok[2];
-#pragma unroll
-    for (int tg = 0; tg < 2; ++tg) tok[tg] = ts + 16 * tg + js < seg_end ? 16 * tg + js : 0;
     const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
     const size_t row0 = (size_t)id * bs + (ts - (int)lb * bs);
     p.base = a.kv + row0 * kD;
-#pragma unroll
-    for (int tg = 0; tg < 2; ++tg) p.voff[tg] = (uint32_t)(tok[tg] * kD + 8 * g) * 2u;
+    p.nvalid = seg_end - ts;
     return p;
   };
   auto issue = [&](const Plan& p, int i) {
     const int blk = w + kWaves * i;
-    const int tg = blk >= kKSteps ? 1 : 0, kk = blk - tg * kKSteps;
-    load_to_lds(p.base + 32 * kk, tg ? p.voff[1] : p.voff[0],
-                __builtin_amdgcn_readfirstlane(p.slot + (uint32_t)blk * 1024));
+    const int rb8 = blk / kColBlocks, cb = blk - rb8 * kColBlocks;
+    const uint32_t voff = 8 * rb8 + cr < p.nvalid ? lane_row_off + (uint32_t)(8 * rb8 * kD * 2)
+                                                  : lane_first_off;
+    load_to_lds(p.base + 64 * cb, voff, __builtin_amdgcn_readfirstlane(block_lds(p.slot, blk)));
   };
   auto stage = [&](int k) {
     const int ts = seg_start + kTile * k;
     const uint32_t slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
-    int tok[2];
-#pragma unroll
-    for (int tg = 0; tg < 2; ++tg) tok[tg] = ts + 16 * tg + js < seg_end ? 16 * tg + js : 0;
     if constexpr (kBlockUniform) {
       // 32 tokens from a 32-aligned start share one block: a uniform base row.
-      const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
-      const size_t row0 = (size_t)btc[lb] * bs + (ts - (int)lb * bs);
-      const uint16_t* base = a.kv + row0 * kD;
-      uint32_t voff[2];
+      const Plan p = prep(k, btc[gqa::fastdiv((uint32_t)ts, a.bs_div)]);
 #pragma unroll
-      for (int tg = 0; tg < 2; ++tg) voff[tg] = (uint32_t)(tok[tg] * kD + 8 * g) * 2u;
-#pragma unroll
-      for (int i = 0; i < kStageLoads; ++i) {
-        const int blk = w + kWaves * i;
-        const int tg = blk >= kKSteps ? 1 : 0, kk = blk - tg * kKSteps;
-        load_to_lds(base + 32 * kk, tg ? voff[1] : voff[0],
-                    __builtin_amdgcn_readfirstlane(slot + (uint32_t)blk * 1024));
-      }
+      for (int i = 0; i < kStageLoads; ++i) issue(p, i);
     } else {
       // The tile's tokens span blocks lb_lo .. lb_hi: fetch their ids with
-      // uniform loads and let each lane take its own.
+      // uniform loads and let each lane take its own rows (one per row block).
       const int t_hi = min(ts + kTile, seg_end) - 1;
       const int lb_lo = (int)gqa::fastdiv((uint32_t)ts, a.bs_div);
       const int lb_hi = (int)gqa::fastdiv((uint32_t)t_hi, a.bs_div);
-      int lbl[2];
-      size_t row[2] = {0, 0};
+      int tok[4], lbl[4];
+      size_t row[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int tg = 0; tg < 2; ++tg) lbl[tg] = (int)gqa::fastdiv((uint32_t)(ts + tok[tg]), a.bs_div);
+      for (int rb8 = 0; rb8 < 4; ++rb8) {
+        tok[rb8] = ts + 8 * rb8 + cr < seg_end ? 8 * rb8 + cr : 0;
+        lbl[rb8] = (int)gqa::fastdiv((uint32_t)(ts + tok[rb8]), a.bs_div);
+      }
       for (int q = lb_lo; q <= lb_hi; ++q) {
         const size_t id = (size_t)btc[q];
 #pragma unroll
-        for (int tg = 0; tg < 2; ++tg) row[tg] = lbl[tg] == q ? id : row[tg];
+        for (int rb8 = 0; rb8 < 4; ++rb8) row[rb8] = lbl[rb8] == q ? id : row[rb8];
       }
-      const uint16_t* src[2];
+      const uint16_t* src[4];
 #pragma unroll
-      for (int tg = 0; tg < 2; ++tg)
-        src[tg] = a.kv + (row[tg] * bs + (ts + tok[tg] - lbl[tg] * bs)) * kD + 8 * g;
+      for (int rb8 = 0; rb8 < 4; ++rb8)
+        src[rb8] = a.kv + (row[rb8] * bs + (ts + tok[rb8] - lbl[rb8] * bs)) * kD + 8 * cc;
 #pragma unroll
       for (int i = 0; i < kStageLoads; ++i) {
         const int blk = w + kWaves * i;
-        const int tg = blk >= kKSteps ? 1 : 0, kk = blk - tg * kKSteps;
-        load_to_lds((tg ? src[1] : src[0]) + 32 * kk,
-                    __builtin_amdgcn_readfirstlane(slot + (uint32_t)blk * 1024));
+        const int rb8 = blk / kColBlocks, cb = blk - rb8 * kColBlocks;
+        load_to_lds(src[rb8] + 64 * cb, __builtin_amdgcn_readfirstlane(block_lds(slot, blk)));
       }
     }
   };
@@ -365,7 +386,8 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
       // Operand reads run kQKAhead k-steps ahead of their MFMAs (the
       // scheduling barriers keep the compiler from sinking them to their use).
       auto read_k = [&](int kk, int tg) -> uint4 {
-        return *reinterpret_cast<const uint4*>(T + (tg * kKSteps + kk) * 1024 + 16 * kslot);
+        return *reinterpret_cast<const uint4*>(T + qoff[kk & 1] + 2 * kRowBlockBytes * tg +
+                                               1024 * (kk >> 1));
       };
       f32x4_t c[2][2];
 #pragma unroll
@@ -400,17 +422,14 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
 
       // V operands for PV, read kPVAhead column blocks ahead of their MFMAs;
       // the first ones are issued before the softmax. Lane (j, g) supplies
-      // token 4g + j/4 (and 16 more), dims 16nb + 4(j%4) .. +4 of the A-order
-      // tile; the transposing read hands lane x the four tokens of dim 16nb + x.
-      const int rr = 4 * g + (j >> 2);
+      // token 4g + j/4 (and 16 more: two row blocks on), dims 16nb + 4(j%4)
+      // .. +4; the transposing read hands lane x the four tokens of dim
+      // 16nb + x.
       auto read_v = [&](int nb) -> bf16x8_t {
-        const int kk = nb >> 1;
-        const int gg = 2 * (nb & 1) + ((j & 3) >> 1);
-        const uint32_t off =
-            (uint32_t)kk * 1024 + 16u * (uint32_t)(16 * gg + (rr ^ ((gg & 1) << 3))) + 8u * (j & 1);
+        const uint32_t off = voff4[nb & 3] + 1024u * (uint32_t)(nb >> 2);
         const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off));
-        const bf16x4_t v1 =
-            __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off + kKSteps * 1024));
+        const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4_t*)(T + off + 2 * kRowBlockBytes));
         return bf16x8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
       };
       bf16x8_t vr[kPVAhead + 1];

@@ -84,8 +84,11 @@ def test_m0_only_in_inline_asm(asm, mangled):
     assert not re.search(r"\bm0\b", outside)
 
 
-# LDS byte offset of the restart votes: they follow the kDepth x 36 KiB tile ring.
-VOTE_LDS = "0x24000"
+def is_vote_address(line):
+    """The restart votes follow the tile ring (kDepth tiles of ~36 KiB): the only
+    LDS data at byte offsets of 128 KiB and up, added as an immediate."""
+    m = re.search(r"s_add\w*\s+s\d+,\s*s\d+,\s*0x([0-9a-f]+)", line)
+    return bool(m) and int(m.group(1), 16) >= 0x20000
 
 
 @pytest.mark.parametrize("mangled", KERNELS)
@@ -95,14 +98,14 @@ def test_restart_ballot_sees_every_lane(asm, mangled):
     # lane-0 branch narrows the exec mask: inside it, it would see lane 0 only.
     lines = kernel_body(asm, mangled).split("\n")
     stores = [i for i, ln in enumerate(lines)
-              if "ds_write_b32" in ln and any(VOTE_LDS in p for p in lines[max(0, i - 4):i])]
+              if "ds_write_b32" in ln and any(is_vote_address(p) for p in lines[max(0, i - 4):i])]
     assert stores, "restart vote store not found"
     for i in stores:
         # The branch narrows exec with s_and_saveexec or by writing exec.
         k = max(k for k in range(i) if re.search(r"s_and_saveexec|s_(mov|and)_b64 exec,", lines[k]))
         between = [ln for ln in lines[k:i] if re.search(r"\bv_cmp", ln)]
         assert not between, f"ballot evaluated under the lane-0 exec mask: {between}"
-        assert any(re.search(r"v_cmp\w*\s+vcc", ln) for ln in lines[max(0, k - 8):k]), \
+        assert any(re.search(r"v_cmp\w*\s+vcc", ln) for ln in lines[max(0, k - 30):k]), \
             "ballot not found before the lane-0 branch"
 
 
