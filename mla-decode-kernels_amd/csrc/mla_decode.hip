@@ -3,44 +3,67 @@
 // one shared latent cache of 576-dim rows; values are the rows' first 512
 // dims. Semantics and layouts: include/mla_decode.h.
 //
-// Work decomposition. A workgroup of 4 waves (one per SIMD) owns 128 query
-// rows (a row group) of one request and a range of its tokens; each wave owns
-// 32 rows as two 16-row MFMA column blocks. All rows share the cache rows, so
-// each 32-token tile (36 KiB) is read from HBM once per workgroup: the waves
-// copy it cooperatively, HBM -> LDS (global_load_lds_dwordx4, no registers),
-// into a ring of kDepth slots with kDepth - 1 tiles in flight, and every wave
-// computes from LDS. Two launches share this tile walk (mla_piece):
+// Work decomposition. A workgroup of 8 waves (two per SIMD) owns 128 query
+// rows (a row group) of one request and a range of its tokens. All rows share
+// the cache rows, so each 32-token tile (36 KiB) is read from HBM once per
+// workgroup: the waves copy it cooperatively, HBM -> LDS
+// (global_load_lds_dwordx4, no registers), into a ring of kDepth slots, and
+// every wave computes from LDS. Two launches share this tile walk (mla_piece):
 //   fixed splits  grid (row groups, B, num_splits), split s of each request;
 //   balanced      one workgroup per CU and row group, each taking an equal
 //                 share of the batch's request-ordered tiles (a plan kernel
 //                 computes the tile prefix sums on the device), walked piece
 //                 by piece; requests cut between shares are merged after.
 //
+// The two matrix products of a tile are split between the waves along
+// different axes, which keeps each wave's registers at what two waves per
+// SIMD can hold (256):
+//   QK^T + softmax  wave w scores its 16 query rows 16w .. 16w + 15 against
+//          the tile's 32 tokens (Q^T of those rows in registers) and writes
+//          the rows' bf16 probabilities to a P buffer in LDS;
+//   PV     wave w accumulates O[all 128 rows][dims 64w .. 64w + 63] from the
+//          P buffer and the tile's column block w (128 fp32 accumulators).
+// A tile's PV needs every wave's probabilities, so the walk is pipelined over
+// intervals: interval s scores tile s into P buffer s % 2 while accumulating
+// tile s - 1 from P buffer (s - 1) % 2, with one workgroup barrier per
+// interval. Waves 0-3 accumulate first and score second, waves 4-7 the other
+// way round, so the two waves of a SIMD keep the matrix unit busy through each
+// other's softmax. The ring holds tile s - 1 (PV), tile s (QK), tile s + 1
+// (landing) and tile s + 2 (copied during interval s): 4 x 36 KiB + 2 x 8 KiB
+// of P = 160 KiB, the whole LDS.
+//
 // LDS tile layout: 4 row blocks of 8 tokens, each 9 column blocks of 1 KiB
-// (8 rows x 128 bytes = 64 dims) plus 16 bytes, so that consecutive row
-// blocks start 16 bytes apart modulo the 256-byte bank cycle; within a column
-// block, row r sits at 128 r and its 16-byte chunk c at position
-// c ^ chunk_swz(r). Each copy instruction fills one column block: 8 lanes per
-// row read that row's 128 contiguous bytes from HBM (a copy of 16 rows x 64
-// bytes per instruction streamed at ~4.5 TB/s, 8 x 128 bytes at ~6.2 TB/s,
-// measured on MI355X), and the swizzle only permutes lanes within a row.
-// Both operand reads below are free of bank conflicts in this layout (the
-// QK ds_read_b128 phases of 16 lanes and the PV ds_read_b64_tr_b16 groups),
-// and both address as a per-lane base plus a per-step immediate.
+// (8 rows x 128 bytes = 64 dims), so column block cb of row block rb8 is the
+// tile's 1 KiB block 9 rb8 + cb; within a column block, row r sits at 128 r and
+// its 16-byte chunk c at position c ^ chunk_swz(rb8, r). Each copy
+// instruction fills one column block: 8 lanes per row read that row's 128
+// contiguous bytes from HBM (a copy of 16 rows x 64 bytes per instruction
+// streamed at ~4.5 TB/s, 8 x 128 bytes at ~6.2 TB/s, measured on MI355X), and
+// the swizzle only permutes lanes within a row. The swizzle makes both operand
+// reads free of bank conflicts under the LDS rules measured on MI355X (64
+// banks of 4 bytes; bank-conflict counters over single-pattern probes):
+// ds_read_b128 serves a wave in 4 phases of 16 lanes, lane l in phase
+// 2 (l / 32) + parity((l / 4) % 8) (lane 0 shares its phase with lanes 1-3,
+// 12-15 and 20-27), free of conflicts when the phase's 16-byte bank quads
+// (addr / 16) % 16 differ; ds_read_b64 and ds_read_b64_tr_b16 serve lanes
+// 0-31 and 32-63, free when (addr / 8) % 32 differ.
 //
 //   QK^T   S^T[16 tok x 16 rows] = K[tok x 576] . Q^T[576 x 16 rows]: 18
-//          MFMAs per token group and row block; A from LDS (lane: token j,
-//          dims 32 kk + 8 g; shared by both row blocks), B = Q^T in registers
-//          (lane: row j, dims 32 kk + 8 g).
-//   softmax on the C layout (lane: row j, tokens 4 g + e), base 2, fp32,
-//          against a per-row reference max fixed at the row's first live
+//          v_mfma_f32_16x16x32_bf16 per 16-token group; A from LDS (lane:
+//          token j, dims 32 kk + 8 g), B = Q^T in registers (lane: row j,
+//          dims 32 kk + 8 g).
+//   softmax on the C layout (lane: row j, tokens 16 tg + 4 g + e), base 2,
+//          fp32, against a per-row reference max fixed at the row's first live
 //          tile (see kRefSlack); P rounded to bf16, l sums the rounded values.
-//   PV     O[16 rows x 512] += P[rows x 32 tok] . V[32 tok x 512]: 32
-//          v_mfma_f32_16x16x32_bf16 per row block (k-slot 8g+e -> token
-//          4g+e, 8g+4+e -> token 16+4g+e); B read from the same LDS tile with
-//          ds_read_b64_tr_b16 (lane x of a 16-lane group supplies token
-//          4g + x/4, dims 16nb + 4(x%4) .. +4; the transpose hands lane x the
-//          four tokens of dim 16nb + x).
+//          P buffer: row R at 64 R, 16-byte chunk c (tokens 8c .. 8c + 7) at
+//          position c ^ (-(R / 4) % 4) (conflict-free ds_read_b128 A reads).
+//   PV     O[16 rows x 16 dims] += P[16 rows x 32 tok] . V[32 tok x 16 dims]:
+//          8 row blocks x 4 column blocks of v_mfma_f32_16x16x32_bf16, k-slot
+//          8 g + e = token 8 g + e; A = one ds_read_b128 of the P buffer
+//          (lane: row j, chunk g), B = two ds_read_b64_tr_b16 of the tile
+//          (lane x of 16-lane group g supplies token 8 g + 4 h + x / 4, dims
+//          16 nb + 4 (x % 4) .. +4; the transpose hands lane x the four tokens
+//          of dim 16 nb + x).
 //
 // Splits and shares cut requests at multiples of 32 tokens; the merges fold
 // the pieces in order (log-sum-exp), so results are bitwise reproducible.
@@ -49,6 +72,7 @@
 #include "mla_decode.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mla {
 
@@ -63,25 +87,35 @@ constexpr int kD = MLA_DECODE_HEAD_DIM;     // 576
 constexpr int kDV = MLA_DECODE_HEAD_DIM_V;  // 512
 constexpr int kKSteps = kD / 32;            // 18 QK k-steps
 constexpr int kTile = 32;                   // tokens per tile
-constexpr int kWaves = 4;
-constexpr int kRowsPerWave = 32;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWave = 16;                      // QK^T rows of a wave
 constexpr int kRowsPerGroup = kWaves * kRowsPerWave;  // 128
+constexpr int kRowBlocks = kRowsPerGroup / 16;        // 8 PV row blocks
 constexpr int kTileBlocks = 2 * kKSteps;              // 36 blocks of 1 KiB
 constexpr int kColBlocks = kD / 64;                   // 9 per row block of 8 tokens
-constexpr int kRowBlockBytes = kColBlocks * 1024 + 16;
-constexpr int kTileBytes = 4 * kRowBlockBytes;
-constexpr int kStageLoads = kTileBlocks / kWaves;     // 9 per wave per tile
-// Tiles in the LDS ring: while a tile is consumed, the next kDepth - 1 are in
-// flight from HBM (about 100 KiB per CU, enough to cover the latency at this
-// CU's share of the bandwidth).
-constexpr int kDepth = 4;
-constexpr int kNB = kDV / 16;                         // 32 PV column blocks
-static_assert(kTileBlocks % kWaves == 0, "staging blocks must split evenly");
+constexpr int kRowBlockBytes = kColBlocks * 1024;
+constexpr int kTileBytes = 4 * kRowBlockBytes;        // 36 KiB
+// Copy instructions per wave per tile: blocks w, w + 8, ...; waves below
+// kWavesHi take one more.
+constexpr int kLoadsHi = (kTileBlocks + kWaves - 1) / kWaves;  // 5
+constexpr int kLoadsLo = kTileBlocks / kWaves;                 // 4
+constexpr int kWavesHi = kTileBlocks % kWaves;                 // 4
+constexpr int kDepth = 4;                                      // ring slots
+constexpr int kPBytes = kRowsPerGroup * kTile * 2;             // one P buffer, 8 KiB
+constexpr int kLdsBytes = kDepth * kTileBytes + 2 * kPBytes;   // 160 KiB
+constexpr int kNBw = kDV / kWaves / 16;                        // 4 PV column blocks per wave
+static_assert(kDV / kWaves == 64, "wave w accumulates the tile's column block w");
 static_assert(kTileBlocks == 4 * kColBlocks, "a tile is 4 row blocks of 9 column blocks");
+static_assert(kLdsBytes <= 160 * 1024, "the ring and the P buffers fill the LDS");
+static_assert(kWavesHi * 2 <= kWaves, "the waves that take kLoadsHi copies accumulate first");
 
-// Position XOR of row r's 16-byte chunks in a column block (a table found by
-// an exhaustive bank-conflict check of both operand reads over this layout).
-__device__ __forceinline__ int chunk_swz(int r) { return (int)((0x46226400u >> (4 * r)) & 7u); }
+// Position XOR of row r's 16-byte chunks in a column block of row block rb8
+// (the table depends on rb8's parity; found by a search over tables that
+// checks both operand reads against the measured LDS phase rules above).
+__device__ __forceinline__ int chunk_swz(int rb8, int r) {
+  return (int)((0x0052246637751143ull >> (4 * (8 * (rb8 & 1) + r))) & 7u);
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -109,27 +143,21 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& u) {
   return __builtin_bit_cast(bf16x8_t, u);
 }
 
-// One row block's running state; lane (j, g): m and lsum of row j (lsum over
-// this lane's token slots only), o[nb][e] = O[row 4g + e][dim 16 nb + j].
-struct RowState {
-  float m, lsum;
-  f32x4_t o[kNB];
-};
-
 // A row's probabilities are taken relative to a reference max that is set by
 // the first tile holding a live key of the row and then kept: rescaling the
-// 32 x 512 fp32 accumulators (all 256 accumulation registers of the lane) on
-// every new max would cost more than the tile's matrix work, and any
-// conditional update of them inside the tile loop makes the compiler copy them
-// on every tile. Probabilities stay below 2^kRefSlack; if a later tile beats a
-// row's reference by more, the workgroup runs its split a second time against
-// the rows' true maxima (the values are exact either way; only that split's
-// time doubles).
+// 128 x 64 fp32 accumulators of a wave (half of its registers) on every new
+// max would cost more than the tile's matrix work, and any conditional update
+// of them inside the tile loop makes the compiler copy them on every tile.
+// Probabilities stay below 2^kRefSlack; if a later tile beats a row's
+// reference by more, the workgroup runs its split a second time against the
+// rows' true maxima (the values are exact either way; only that split's time
+// doubles).
 constexpr float kRefSlack = 32.f;
-// LDS operand reads run this many MFMA steps ahead of their use: QK k-steps
-// (4 MFMAs each) and PV column blocks (2 MFMAs each).
-constexpr int kQKAhead = 2;
-constexpr int kPVAhead = 4;
+// LDS operand reads run ahead of their use: QK reads through a ring of
+// kKRing single-read slots (each read kKRing - 1 MFMAs ahead), PV P-operand
+// reads kPAhead row blocks (4 MFMAs each) ahead.
+constexpr int kKRing = 5;
+constexpr int kPAhead = 2;
 
 // Direct HBM -> LDS copies of 16 bytes per lane (global_load_lds_dwordx4):
 // lane x's bytes land at LDS byte address lds + 16 x; lds must be
@@ -161,8 +189,8 @@ __device__ __forceinline__ void load_to_lds(const uint16_t* src, uint32_t lds) {
 }
 
 // Waits until at most kInFlight of this wave's direct loads are outstanding
-// (they complete in issue order), then joins the workgroup barrier; LDS reads
-// and writes are not moved across it.
+// (they complete in issue order) and its LDS writes are done, then joins the
+// workgroup barrier; LDS reads and writes are not moved across it.
 template <int kInFlight>
 __device__ __forceinline__ void publish_barrier() {
   static_assert(kInFlight >= 0 && kInFlight < 64, "vmcnt holds 6 bits");
@@ -196,57 +224,115 @@ struct PieceOut {
   int st_stride;
 };
 
+// After a pass, P buffer 1 (first written in the second interval of a pass,
+// two barriers after any pass starts) holds the restart votes and the rows'
+// final sums.
+constexpr int kStatL = 0;    // 128 floats: row sums
+constexpr int kVotes = 512;  // 8 ints
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
+typedef __attribute__((address_space(3))) u32x2_t lds_u32x2_t;
+
+// LDS accesses by 32-bit LDS byte address.
+__device__ __forceinline__ u32x4_t lds_load16(uint32_t addr) {
+  return *(const lds_u32x4_t*)(uintptr_t)addr;
+}
+__device__ __forceinline__ void lds_store8(uint32_t addr, u32x2_t v) {
+  *(lds_u32x2_t*)(uintptr_t)addr = v;
+}
+__device__ __forceinline__ bf16x4_t lds_load_tr(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(uintptr_t)addr);
+}
+__device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& u) {
+  return __builtin_bit_cast(bf16x8_t, u);
+}
+
+// Hands x back through an empty asm statement, so that the compiler treats it
+// as a new value: applied to the lane's operand offsets at the top of every
+// interval, it keeps values derived from them (offset ^ constant, one per
+// matrix step) from being hoisted out of the tile loop, where they would
+// outgrow the register budget of two waves per SIMD.
+__device__ __forceinline__ void refresh(uint32_t& x) { asm volatile("" : "+v"(x)); }
+
 // The workgroup's 128 query rows (row group rg) of request b against tokens
 // [seg_start, seg_end) of the request's S live tokens. Every wave of the
 // workgroup calls it with the same arguments (its barriers are workgroup-wide).
 template <bool kBlockUniform>
-__device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTileBytes],
-                                          int* restart_vote, int b, int rg, int S, int seg_start,
-                                          int seg_end, PieceOut po) {
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+__device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b, int rg, int S,
+                                          int seg_start, int seg_end, PieceOut po) {
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  // Every lane-dependent value below derives from tid, refreshed here so that
+  // none of them is hoisted out of a caller's loop over pieces.
+  uint32_t tid = threadIdx.x;
+  refresh(tid);
+  const int lane = (int)(tid & 63);
+  const int w = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const int j = lane & 15, g = lane >> 4;
-  // Copies: lane x fills row cr = x / 8 of a column block, position x % 8,
-  // from that row's chunk cc = (x % 8) ^ chunk_swz(cr).
-  const int cr = lane >> 3, cc = (lane & 7) ^ chunk_swz(lane >> 3);
-  // Tile-relative LDS offsets of this lane's operands (plus a per-step
-  // immediate): QK A operand of token group tg, k-step parity par (token
-  // 16 tg + j, chunk 4 par + g of column block kk / 2), and PV B operand of
-  // column-block quarter q = nb % 4 (tokens 4 g + j / 4 (+16), dims
-  // 16 nb + 4 (j % 4) .. +4: chunk 2 q + (j % 4) / 2, half j % 2).
-  // (Token group 1 is two row blocks on: an immediate.)
-  uint32_t qoff[2], voff4[4];
-#pragma unroll
-  for (int par = 0; par < 2; ++par)
-    qoff[par] = (uint32_t)((j >> 3) * kRowBlockBytes + (j & 7) * 128 +
-                           16 * ((4 * par + g) ^ chunk_swz(j & 7)));
+  const uint32_t smem_lds = (uint32_t)(uintptr_t)(lds_u8*)smem;
+  const uint32_t pbuf_lds = smem_lds + kDepth * kTileBytes;  // P buffer t at + t * kPBytes
+  uint8_t* const pbuf1 = smem + kDepth * kTileBytes + kPBytes;
+
+  // Copies. Wave w copies row blocks of parity par = w % 2 only (row blocks
+  // par and par + 2: 18 column blocks m, rb8 = par + 2 (m / 9), cb = m % 9),
+  // taking m = w / 2 + 4 i (i < 5, m < 18): 5 copies for waves 0-3, 4 for
+  // waves 4-7. Lane x fills row cr = x / 8 of a column block, position x % 8,
+  // from that row's chunk (x % 8) ^ chunk_swz(par, cr): one source offset
+  // per lane, ro (the row's offset; ro & 0x70 is its chunk's offset in row 0).
+  const int par = w & 1, cu = w >> 1;
+  uint32_t ro = (uint32_t)((lane >> 3) * kD + 8 * ((lane & 7) ^ chunk_swz(par, lane >> 3))) * 2u;
+  // Tile-relative LDS offsets of this lane's operands (plus per-step
+  // immediates or XORs; a slot's address has its low 10 bits clear, so a XOR
+  // applies to slot + offset as well):
+  //  QK A operand of token 16 tg + j, chunk 4 par + g of column block kk / 2
+  //    (k-step parity flips bit 6: ^ 64; token group 1 is two row blocks on);
+  //  PV B operand of row block g, column block w, rows 4 h + j / 4, chunk
+  //    2 nb + (j % 4) / 2, half j % 2 (nb flips bits 5-6: ^ 32 nb);
+  //  P buffer: A operand row 16 rb + j, chunk g (+ 1 KiB per row block); the
+  //    lane's probabilities, row 16 w + j, chunks 2 tg + g / 2, half g % 2
+  //    (tg flips bit 5: ^ 32).
+  uint32_t qoff = (uint32_t)((j >> 3) * kRowBlockBytes + (j & 7) * 128 +
+                             16 * (g ^ chunk_swz(j >> 3, j & 7)));
+  uint32_t vx0, vx1;
   {
-    const int vr = 4 * (g & 1) + (j >> 2);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      voff4[q] = (uint32_t)((g >> 1) * kRowBlockBytes + vr * 128 +
-                            16 * ((2 * q + ((j & 3) >> 1)) ^ chunk_swz(vr)) + 8 * (j & 1));
+    const int r0 = j >> 2, r1 = 4 + (j >> 2);
+    const int base = g * kRowBlockBytes + w * 1024 + 8 * (j & 1);
+    vx0 = (uint32_t)(base + r0 * 128 + 16 * (((j & 3) >> 1) ^ chunk_swz(g, r0)));
+    vx1 = (uint32_t)(base + r1 * 128 + 16 * (((j & 3) >> 1) ^ chunk_swz(g, r1)));
   }
-  // Waves whose rows all lie past R compute on zero queries (their results are
-  // not stored): a wave-dependent branch around the tile work would make the
+  // (The copy row and the P buffer offsets are recomputed from tid where
+  // they are used: three fewer registers held through the tile loop.)
+  auto lane_cr = [&]() -> int { return (int)((tid >> 3) & 7); };
+  auto pr_off = [&]() -> uint32_t {
+    const uint32_t jj = tid & 15, gg = (tid >> 4) & 3;
+    return jj * 64 + 16 * (gg ^ (-(jj >> 2) & 3));
+  };
+  auto pw_off = [&]() -> uint32_t {
+    const uint32_t jj = tid & 15, gg = (tid >> 4) & 3;
+    return (uint32_t)w * 1024 + jj * 64 + 16 * ((gg >> 1) ^ (-(jj >> 2) & 3)) + 8 * (gg & 1);
+  };
+
+  // Waves whose rows all lie past R score zero queries (their results are not
+  // stored): a wave-dependent branch around the tile work would make the
   // compiler copy the accumulators on every tile.
   const int row0 = rg * kRowsPerGroup + w * kRowsPerWave;
   const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
 
   // Q^T as the B operand, all 18 k-steps in registers (lane: row j, dims
-  // 32 kk + 8 g); and each lane's key limit for its row j.
-  uint4 qf[2][kKSteps];
-  int lim[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int r = row0 + 16 * rb + j;
+  // 32 kk + 8 g); and the lane's key limit for its row j, less 4 g (token
+  // 16 tg + 4 g + e of the tile at ts is live iff 16 tg + e < lim4 - ts).
+  uint4 qf[kKSteps];
+  int lim4;
+  {
+    const int r = row0 + j;
     const bool live = r < a.R;
     const uint16_t* qrow = a.q + ((size_t)b * a.R + (live ? r : 0)) * kD + 8 * g;
 #pragma unroll
     for (int kk = 0; kk < kKSteps; ++kk)
-      qf[rb][kk] = live ? *reinterpret_cast<const uint4*>(qrow + 32 * kk) : make_uint4(0, 0, 0, 0);
+      qf[kk] = live ? *reinterpret_cast<const uint4*>(qrow + 32 * kk) : make_uint4(0, 0, 0, 0);
     const int qi = live ? r / a.h_q : 0;
-    lim[rb] = min(seg_end, a.causal ? S - (a.s_q - 1 - qi) : S);
+    lim4 = min(seg_end, a.causal ? S - (a.s_q - 1 - qi) : S) - 4 * g;
   }
   // Let the Q loads land here: a wait left to their first use would sit inside
   // the tile loop, where it would also wait for every tile copy in flight.
@@ -258,302 +344,309 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
   const __attribute__((address_space(4))) int* btc =
       (const __attribute__((address_space(4))) int*)bt;
   const int bs = a.block_size;
-  typedef __attribute__((address_space(3))) uint8_t lds_u8;
-  const uint32_t tiles_lds = (uint32_t)(uintptr_t)(lds_u8*)&tiles[0][0];
 
-  // Staging of tile k into ring slot k % kDepth: wave w copies column blocks
-  // blk = w + 4 i (i < 9): row block rb8 = blk / 9 (tokens 8 rb8 .. +8),
-  // column block cb = blk % 9 (dims 64 cb .. +64). A lane's row is
-  // 8 rb8 + cr; tokens at or past seg_end read the tile's first token instead
-  // (masked later), so nothing outside the request's live cache rows is
-  // touched. Block ids come from scalar loads, which keeps the vector memory
-  // counter for the copies alone.
-  // The refill copies of the block-uniform path are issued two per QK^T
-  // k-step rather than in one burst after the barrier (a burst queues behind
-  // the other waves' copies and holds the wave); Plan carries what they need,
-  // and the block id is loaded one iteration ahead, before the barrier, so
-  // that its scalar-load latency overlaps the wait for the landing tile.
-  // (Plan holds only wave-uniform values: a lane's source offset is its row
-  // offset, or its chunk of the tile's first token for rows past seg_end.)
-  struct Plan {
-    const uint16_t* base;
-    int nvalid;
-    uint32_t slot;
-  };
-  const uint32_t lane_row_off = (uint32_t)(cr * kD + 8 * cc) * 2u, lane_first_off = 16u * cc;
+  // Staging of tile k into ring slot k % kDepth. Tokens at or past seg_end
+  // read the tile's first token instead (masked later), so nothing outside
+  // the request's live cache rows is touched. Block ids come from scalar
+  // loads, which keeps the vector memory counter for the copies alone. A
+  // refill goes out at the start of an interval, right after the barrier
+  // that freed its slot; its block id is loaded one interval ahead, before
+  // that barrier, so that the scalar-load latency overlaps the wait for the
+  // landing tile.
   auto block_id = [&](int k) -> int {
     return btc[gqa::fastdiv((uint32_t)(seg_start + kTile * k), a.bs_div)];
   };
-  // The LDS address of column block blk of the slot at `slot`.
-  auto block_lds = [&](uint32_t slot, int blk) -> uint32_t {
-    const int rb8 = blk / kColBlocks, cb = blk - rb8 * kColBlocks;
-    return slot + (uint32_t)(rb8 * kRowBlockBytes + cb * 1024);
-  };
-  auto prep = [&](int k, int id) -> Plan {
+  auto stage = [&](int k, int id) {
     const int ts = seg_start + kTile * k;
-    Plan p;
-    p.slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
-    const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
-    const size_t row0 = (size_t)id * bs + (ts - (int)lb * bs);
-    p.base = a.kv + row0 * kD;
-    p.nvalid = seg_end - ts;
-    return p;
-  };
-  auto issue = [&](const Plan& p, int i) {
-    const int blk = w + kWaves * i;
-    const int rb8 = blk / kColBlocks, cb = blk - rb8 * kColBlocks;
-    const uint32_t voff = 8 * rb8 + cr < p.nvalid ? lane_row_off + (uint32_t)(8 * rb8 * kD * 2)
-                                                  : lane_first_off;
-    load_to_lds(p.base + 64 * cb, voff, __builtin_amdgcn_readfirstlane(block_lds(p.slot, blk)));
-  };
-  auto stage = [&](int k) {
-    const int ts = seg_start + kTile * k;
-    const uint32_t slot = tiles_lds + (uint32_t)(k % kDepth) * kTileBytes;
+    const uint32_t slot = smem_lds + (uint32_t)(k % kDepth) * kTileBytes;
     if constexpr (kBlockUniform) {
       // 32 tokens from a 32-aligned start share one block: a uniform base row.
-      const Plan p = prep(k, btc[gqa::fastdiv((uint32_t)ts, a.bs_div)]);
+      const uint32_t lb = gqa::fastdiv((uint32_t)ts, a.bs_div);
+      const uint16_t* base = a.kv + ((size_t)id * bs + (ts - (int)lb * bs)) * kD;
+      const int nvalid = seg_end - ts;
+      auto copy = [&](int i) {
+        const int m = cu + 4 * i, hi = m >= kColBlocks ? 1 : 0;
+        const int rb8 = par + 2 * hi, cb = m - kColBlocks * hi;
+        // (The row block's offset stays in the lane offset: a row past
+        // seg_end must land on the tile's first row, not the block's.)
+        const uint32_t voff = lane_cr() < nvalid - 8 * rb8 ? ro + (uint32_t)(8 * rb8 * kD * 2)
+                                                            : (ro & 0x70u);
+        load_to_lds(base + 64 * cb, voff,
+                    __builtin_amdgcn_readfirstlane(slot + (kColBlocks * rb8 + cb) * 1024));
+      };
 #pragma unroll
-      for (int i = 0; i < kStageLoads; ++i) issue(p, i);
+      for (int i = 0; i < kLoadsLo; ++i) copy(i);
+      if (w < kWavesHi) copy(kLoadsLo);
     } else {
       // The tile's tokens span blocks lb_lo .. lb_hi: fetch their ids with
-      // uniform loads and let each lane take its own rows (one per row block).
+      // uniform loads and let each lane take its own rows (one per row block
+      // of the wave's parity).
       const int t_hi = min(ts + kTile, seg_end) - 1;
       const int lb_lo = (int)gqa::fastdiv((uint32_t)ts, a.bs_div);
       const int lb_hi = (int)gqa::fastdiv((uint32_t)t_hi, a.bs_div);
-      int tok[4], lbl[4];
-      size_t row[4] = {0, 0, 0, 0};
+      int tok[2], lbl[2];
+      size_t row[2] = {0, 0};
 #pragma unroll
-      for (int rb8 = 0; rb8 < 4; ++rb8) {
-        tok[rb8] = ts + 8 * rb8 + cr < seg_end ? 8 * rb8 + cr : 0;
-        lbl[rb8] = (int)gqa::fastdiv((uint32_t)(ts + tok[rb8]), a.bs_div);
+      for (int x = 0; x < 2; ++x) {
+        const int t = 8 * (par + 2 * x) + lane_cr();
+        tok[x] = ts + t < seg_end ? t : 0;
+        lbl[x] = (int)gqa::fastdiv((uint32_t)(ts + tok[x]), a.bs_div);
       }
       for (int q = lb_lo; q <= lb_hi; ++q) {
-        const size_t id = (size_t)btc[q];
+        const size_t bid = (size_t)btc[q];
 #pragma unroll
-        for (int rb8 = 0; rb8 < 4; ++rb8) row[rb8] = lbl[rb8] == q ? id : row[rb8];
+        for (int x = 0; x < 2; ++x) row[x] = lbl[x] == q ? bid : row[x];
       }
-      const uint16_t* src[4];
+      const uint16_t* src[2];
 #pragma unroll
-      for (int rb8 = 0; rb8 < 4; ++rb8)
-        src[rb8] = a.kv + (row[rb8] * bs + (ts + tok[rb8] - lbl[rb8] * bs)) * kD + 8 * cc;
+      for (int x = 0; x < 2; ++x)
+        src[x] = a.kv + (row[x] * bs + (ts + tok[x] - lbl[x] * bs)) * kD + ((ro & 0x70u) >> 1);
+      auto copy = [&](int i) {
+        const int m = cu + 4 * i, hi = m >= kColBlocks ? 1 : 0;
+        const int rb8 = par + 2 * hi, cb = m - kColBlocks * hi;
+        load_to_lds((hi ? src[1] : src[0]) + 64 * cb,
+                    __builtin_amdgcn_readfirstlane(slot + (kColBlocks * rb8 + cb) * 1024));
+      };
 #pragma unroll
-      for (int i = 0; i < kStageLoads; ++i) {
-        const int blk = w + kWaves * i;
-        const int rb8 = blk / kColBlocks, cb = blk - rb8 * kColBlocks;
-        load_to_lds(src[rb8] + 64 * cb, __builtin_amdgcn_readfirstlane(block_lds(slot, blk)));
-      }
+      for (int i = 0; i < kLoadsLo; ++i) copy(i);
+      if (w < kWavesHi) copy(kLoadsLo);
     }
   };
+  // End of an interval: the next tile must have landed (with a refill in
+  // flight, this wave's copies of it stay outstanding), then the barrier.
+  auto publish = [&](bool refill) {
+    if (!refill)
+      publish_barrier<0>();
+    else if (w < kWavesHi)
+      publish_barrier<kLoadsHi>();
+    else
+      publish_barrier<kLoadsLo>();
+  };
 
-  f32x4_t o[2][kNB];
-  float lsum[2];
-  float mref[2] = {kNegInf, kNegInf};  // row j's reference max (log2 units)
-  float mtrue[2] = {kNegInf, kNegInf};  // row j's max over the split so far
-  bool beaten = false;                  // some row's max beat its reference
+  f32x4_t o[kRowBlocks][kNBw];
+  float lsum = 0.f;
+  float mref = kNegInf;   // row j's reference max (log2 units)
+  float mtrue = kNegInf;  // row j's max over the split so far (lane-local)
+  bool beaten = false;    // some row's max beat its reference
+
+  // QK^T and softmax of tile s into P buffer s % 2.
+  auto score = [&](int s) {
+    const uint32_t T = smem_lds + (uint32_t)(s % kDepth) * kTileBytes;
+    const int ts = seg_start + kTile * s;
+    // c[tg][e] = score of token 16 tg + 4 g + e for row j. The tile's 36
+    // operand reads (read n: k-step n / 2, token group n % 2) cycle through a
+    // ring of kKRing registers, each issued kKRing - 1 MFMAs ahead of its use
+    // (the scheduling barriers keep the compiler from sinking them).
+    const uint32_t qa = T + qoff;
+    auto read_k = [&](int n) -> u32x4_t {
+      const int kk = n >> 1, tg = n & 1;
+      return lds_load16((qa ^ (64u * (kk & 1))) + 2 * kRowBlockBytes * tg + 1024 * (kk >> 1));
+    };
+    f32x4_t c[2];
+#pragma unroll
+    for (int tg = 0; tg < 2; ++tg) c[tg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4_t kr[kKRing];
+#pragma unroll
+    for (int n = 0; n < kKRing - 1; ++n) kr[n] = read_k(n);
+#pragma unroll
+    for (int n = 0; n < 2 * kKSteps; ++n) {
+      // The slot refilled here was read by the previous MFMA.
+      if (n + kKRing - 1 < 2 * kKSteps) kr[(n + kKRing - 1) % kKRing] = read_k(n + kKRing - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      c[n & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[n % kKRing]),
+                                                         as_bf16x8(qf[n >> 1]), c[n & 1], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Probabilities against the reference max, rounded to bf16 (l sums the
+    // rounded values). The lane's tokens are live iff 16 tg + e < d; a tile
+    // where that holds for every lane (d >= 20 everywhere) skips the masking.
+    const int d = lim4 - ts;
+    const bool partial = __builtin_amdgcn_ballot_w64(d < 20) != 0;
+    float sc[2][4];
+    float mx = kNegInf;
+    if (partial) {
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sc[tg][e] = 16 * tg + e < d ? c[tg][e] * a.scale_log2e : kNegInf;
+          mx = fmaxf(mx, sc[tg][e]);
+        }
+    } else {
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sc[tg][e] = c[tg][e] * a.scale_log2e;
+          mx = fmaxf(mx, sc[tg][e]);
+        }
+    }
+    // mx is this lane's max (its 8 tokens of row j). The row's first live tile
+    // sets the reference (nothing is accumulated before it, so nothing needs
+    // rescaling); the row's four lanes agree on it.
+    mref = mref == kNegInf ? row_max(mx) : mref;
+    beaten |= mx > mref + kRefSlack;
+    mtrue = fmaxf(mtrue, mx);
+    const float base = mref == kNegInf ? 0.f : mref;
+    const uint32_t pw = pbuf_lds + (uint32_t)(s & 1) * kPBytes + pw_off();
+    float psum = 0.f;
+#pragma unroll
+    for (int tg = 0; tg < 2; ++tg) {
+      uint32_t wd[2];
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        const gqa::bf16x2_t pb = __builtin_convertvector(
+            (float __attribute__((ext_vector_type(2)))){exp2_fast(sc[tg][e] - base),
+                                                        exp2_fast(sc[tg][e + 1] - base)},
+            gqa::bf16x2_t);
+        wd[e / 2] = __builtin_bit_cast(uint32_t, pb);
+        psum = gqa::dot2_bf16(wd[e / 2], 0x3F803F80u, psum);  // + both values (x 1.0)
+      }
+      lds_store8(pw ^ (32u * tg), u32x2_t{wd[0], wd[1]});
+    }
+    lsum += psum;
+  };
+
+  // PV of tile s from P buffer s % 2: o[rb][nb] += P[rows 16 rb .. +16][32
+  // tok] . V[32 tok][dims 64 w + 16 nb .. +16].
+  auto accumulate = [&](int s) {
+    const uint32_t T = smem_lds + (uint32_t)(s % kDepth) * kTileBytes;
+    const uint32_t va0 = T + vx0, va1 = T + vx1;
+    const uint32_t pa_addr = pbuf_lds + (uint32_t)(s & 1) * kPBytes + pr_off();
+    bf16x8_t vv[kNBw];
+#pragma unroll
+    for (int nb = 0; nb < kNBw; ++nb) {
+      const bf16x4_t v0 = lds_load_tr(va0 ^ (32u * nb));
+      const bf16x4_t v1 = lds_load_tr(va1 ^ (32u * nb));
+      vv[nb] = bf16x8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    }
+    u32x4_t pa[kPAhead + 1];
+#pragma unroll
+    for (int rb = 0; rb < kPAhead; ++rb) pa[rb] = lds_load16(pa_addr + 1024 * rb);
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb) {
+      if (rb + kPAhead < kRowBlocks)
+        pa[(rb + kPAhead) % (kPAhead + 1)] = lds_load16(pa_addr + 1024 * (rb + kPAhead));
+      __builtin_amdgcn_sched_barrier(0);
+      const bf16x8_t pv = as_bf16x8(pa[rb % (kPAhead + 1)]);
+#pragma unroll
+      for (int nb = 0; nb < kNBw; ++nb)
+        o[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pv, vv[nb], o[rb][nb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
   // One pass over the split's tiles, accumulating o and lsum against mref.
-  auto pass = [&]() {
+  // Interval kinds: 0 scores tile 0 only, 1 scores tile s and accumulates
+  // tile s - 1, 2 accumulates the last tile only.
+  auto pass = [&](auto pv_first) {
+    constexpr bool kPVFirst = decltype(pv_first)::value;
+    lsum = 0.f;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      lsum[rb] = 0.f;
+    for (int rb = 0; rb < kRowBlocks; ++rb)
 #pragma unroll
-      for (int nb = 0; nb < kNB; ++nb) o[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
+      for (int nb = 0; nb < kNBw; ++nb) o[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (ntiles == 0) return;
     int id_next = 0;
-    if constexpr (kBlockUniform) {
-      if (kDepth - 1 < ntiles) id_next = block_id(kDepth - 1);
-    }
-    // Prologue: tiles 0 .. kDepth - 2 in flight; tile 0 published.
-    for (int k = 0; k < kDepth - 1 && k < ntiles; ++k) stage(k);
-    if (ntiles >= kDepth - 1)
-      publish_barrier<kStageLoads * (kDepth - 2)>();
-    else
-      publish_barrier<0>();
-    for (int k = 0; k < ntiles; ++k) {
-      // Refill the slot consumed in the previous iteration (every wave has
-      // passed the barrier that ended it).
-      const bool refill = k + kDepth - 1 < ntiles;
-      Plan pl;
-      if constexpr (kBlockUniform) {
-        if (refill) pl = prep(k + kDepth - 1, id_next);
-      } else {
-        if (refill) stage(k + kDepth - 1);
-      }
-      const uint8_t* T = tiles[k % kDepth];
-      const int ts = seg_start + kTile * k;
-
-      // QK^T: c[rb][tg][e] = score of token 16 tg + 4 g + e for row j of block rb.
-      // Operand reads run kQKAhead k-steps ahead of their MFMAs (the
-      // scheduling barriers keep the compiler from sinking them to their use).
-      auto read_k = [&](int kk, int tg) -> uint4 {
-        return *reinterpret_cast<const uint4*>(T + qoff[kk & 1] + 2 * kRowBlockBytes * tg +
-                                               1024 * (kk >> 1));
-      };
-      f32x4_t c[2][2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int tg = 0; tg < 2; ++tg) c[rb][tg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      uint4 kr[kQKAhead + 1][2];
-#pragma unroll
-      for (int kk = 0; kk < kQKAhead; ++kk)
-#pragma unroll
-        for (int x = 0; x < 2; ++x) kr[kk][x] = read_k(kk, x);
-#pragma unroll
-      for (int kk = 0; kk < kKSteps; ++kk) {
-        if (kk + kQKAhead < kKSteps) {
-          const int sl = (kk + kQKAhead) % (kQKAhead + 1);
-#pragma unroll
-          for (int x = 0; x < 2; ++x) kr[sl][x] = read_k(kk + kQKAhead, x);
-        }
-        if constexpr (kBlockUniform) {
-          if ((kk & 1) == 0 && refill) issue(pl, kk >> 1);  // copies 0..8 of the refill
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const int sl = kk % (kQKAhead + 1);
-#pragma unroll
-        for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
-            c[rb][tg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                as_bf16x8(kr[sl][tg]), as_bf16x8(qf[rb][kk]), c[rb][tg], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-
-      // V operands for PV, read kPVAhead column blocks ahead of their MFMAs;
-      // the first ones are issued before the softmax. Lane (j, g) supplies
-      // token 4g + j/4 (and 16 more: two row blocks on), dims 16nb + 4(j%4)
-      // .. +4; the transposing read hands lane x the four tokens of dim
-      // 16nb + x.
-      auto read_v = [&](int nb) -> bf16x8_t {
-        const uint32_t off = voff4[nb & 3] + 1024u * (uint32_t)(nb >> 2);
-        const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(T + off));
-        const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (lds_bf16x4_t*)(T + off + 2 * kRowBlockBytes));
-        return bf16x8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-      };
-      bf16x8_t vr[kPVAhead + 1];
-#pragma unroll
-      for (int nb = 0; nb < kPVAhead; ++nb) vr[nb] = read_v(nb);
+    auto interval = [&](auto kind, int s) {
+      constexpr int kKind = decltype(kind)::value;
+      constexpr bool kQK = kKind != 2, kPV = kKind != 0;
+      refresh(tid);
+      refresh(ro);
+      refresh(qoff);
+      refresh(vx0);
+      refresh(vx1);
+      const bool refill = kQK && s + 2 < ntiles;
+      if (refill) stage(s + 2, id_next);
       __builtin_amdgcn_sched_barrier(0);
-
-      // Probabilities against the reference max, rounded to bf16 (l sums the
-      // rounded values).
-      uint32_t pw[2][4];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        float sc[2][4];
-        float mx = kNegInf;
-#pragma unroll
-        for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool valid = ts + 16 * tg + 4 * g + e < lim[rb];
-            sc[tg][e] = valid ? c[rb][tg][e] * a.scale_log2e : kNegInf;
-            mx = fmaxf(mx, sc[tg][e]);
-          }
-        // mx is this lane's max (its 8 tokens of row j). The row's first live
-        // tile sets the reference (nothing is accumulated before it, so
-        // nothing needs rescaling); the row's four lanes agree on it.
-        mref[rb] = mref[rb] == kNegInf ? row_max(mx) : mref[rb];
-        beaten |= mx > mref[rb] + kRefSlack;
-        mtrue[rb] = fmaxf(mtrue[rb], mx);  // lane-local until a second pass
-        const float base = mref[rb] == kNegInf ? 0.f : mref[rb];
-        float psum = 0.f;
-#pragma unroll
-        for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            const gqa::bf16x2_t pb = __builtin_convertvector(
-                (float __attribute__((ext_vector_type(2)))){exp2_fast(sc[tg][e] - base),
-                                                            exp2_fast(sc[tg][e + 1] - base)},
-                gqa::bf16x2_t);
-            const uint32_t wd = __builtin_bit_cast(uint32_t, pb);
-            pw[rb][2 * tg + e / 2] = wd;
-            psum += gqa::bf16_lo(wd) + gqa::bf16_hi(wd);
-          }
-        lsum[rb] += psum;
-      }
-
-      // PV: o[rb][nb] += P[16 rows x 32 tok] . V[32 tok x dims 16nb .. +16].
-#pragma unroll
-      for (int nb = 0; nb < kNB; ++nb) {
-        if (nb + kPVAhead < kNB) vr[(nb + kPVAhead) % (kPVAhead + 1)] = read_v(nb + kPVAhead);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const bf16x8_t pa =
-              as_bf16x8(make_uint4(pw[rb][0], pw[rb][1], pw[rb][2], pw[rb][3]));
-          o[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vr[nb % (kPVAhead + 1)],
-                                                              o[rb][nb], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // The block id the next iteration's copies need, loaded here so that
-      // its latency overlaps the wait below.
+      if constexpr (kPV && kPVFirst) accumulate(s - 1);
+      if constexpr (kQK) score(s);
+      if constexpr (kPV && !kPVFirst) accumulate(s - 1);
+      // The block id of the next interval's refill, loaded here so that its
+      // latency overlaps the wait below.
       if constexpr (kBlockUniform) {
-        if (k + kDepth < ntiles) id_next = block_id(k + kDepth);
+        if (s + 3 < ntiles) id_next = block_id(s + 3);
       }
-      // Tile k + 1 must have landed; the later ones stay in flight.
-      if (refill)
-        publish_barrier<kStageLoads * (kDepth - 2)>();
-      else
-        publish_barrier<0>();
+      publish(refill);
+    };
+    // Prologue: tiles 0 and 1 in flight; tile 0 published.
+    stage(0, kBlockUniform ? block_id(0) : 0);
+    if (ntiles > 1) stage(1, kBlockUniform ? block_id(1) : 0);
+    if constexpr (kBlockUniform) {
+      if (ntiles > 2) id_next = block_id(2);
     }
+    publish(ntiles > 1);
+    interval(std::integral_constant<int, 0>{}, 0);
+    for (int s = 1; s < ntiles; ++s) interval(std::integral_constant<int, 1>{}, s);
+    interval(std::integral_constant<int, 2>{}, ntiles);
+  };
+  auto run_pass = [&]() {
+    if (w < kWaves / 2)
+      pass(std::true_type{});
+    else
+      pass(std::false_type{});
   };
 
-  pass();
+  run_pass();
   // A row whose max beat its reference by more than kRefSlack has overflowed
   // or lost precision: the workgroup (which stages tiles together) runs the
   // split again with every row's reference at its true max (probabilities
   // <= 1, so a second pass always suffices). The ballot is taken with the
-  // whole wave active (each lane holds its own rows' and tokens' flag); only
+  // whole wave active (each lane holds its own row's and tokens' flag); only
   // the store is lane 0's.
+  int* const votes = reinterpret_cast<int*>(pbuf1 + kVotes);
   const bool wave_beaten = __builtin_amdgcn_ballot_w64(beaten) != 0;
-  if (lane == 0) restart_vote[w] = wave_beaten;
+  if (lane == 0) votes[w] = wave_beaten;
   __syncthreads();
-  if (restart_vote[0] | restart_vote[1] | restart_vote[2] | restart_vote[3]) {
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      mref[rb] = row_max(mtrue[rb]);
-    }
-    pass();
+  const uint4 va = *reinterpret_cast<const uint4*>(votes);
+  const uint4 vb = *reinterpret_cast<const uint4*>(votes + 4);
+  if ((va.x | va.y | va.z | va.w | vb.x | vb.y | vb.z | vb.w) != 0) {
+    mref = row_max(mtrue);
+    run_pass();
   }
 
-  // Final (m, l) of the rows this lane's o entries hold: rows 4g + e.
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    float L = lsum[rb] + __shfl_xor(lsum[rb], 16, 64);
-    L += __shfl_xor(L, 32, 64);
-    float Me[4], Le[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      Me[e] = __shfl(mref[rb], 4 * g + e, 64);
-      Le[e] = __shfl(L, 4 * g + e, 64);
+  // Row j's final l (lane (j, g) holds l over its own tokens), published to
+  // every wave through the LDS; its owner writes the row's (m, l) or lse.
+  float L = lsum + __shfl_xor(lsum, 16, 64);
+  L += __shfl_xor(L, 32, 64);
+  float* const stat_l = reinterpret_cast<float*>(pbuf1 + kStatL);
+  if (g == 0) {
+    stat_l[kRowsPerWave * w + j] = L;
+    const int row = row0 + j;
+    if (row < a.R) {
+      if (po.direct) {
+        if (a.lse) {
+          const int qi = row / a.h_q, h = row - qi * a.h_q;
+          a.lse[((size_t)b * a.h_q + h) * a.s_q + qi] = L > 0.f ? mref * kLn2 + logf(L) : kNegInf;
+        }
+      } else {
+        const size_t sx = po.st_base + (size_t)row * po.st_stride;
+        a.ws_m[sx] = L > 0.f ? mref * kLn2 : kNegInf;  // natural-log units
+        a.ws_l[sx] = L;
+      }
     }
+  }
+  __syncthreads();
+  // This wave's o entries: rows 16 rb + 4 g + e, dims 64 w + 16 nb + j.
+#pragma unroll
+  for (int rb = 0; rb < kRowBlocks; ++rb) {
+    const float4 L4 = *reinterpret_cast<const float4*>(stat_l + 16 * rb + 4 * g);
+    const float Le[4] = {L4.x, L4.y, L4.z, L4.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int row = row0 + 16 * rb + 4 * g + e;
+      const int row = rg * kRowsPerGroup + 16 * rb + 4 * g + e;
       if (row >= a.R) continue;
       const size_t br = (size_t)b * a.R + row;
       if (po.direct) {
         const float inv = Le[e] > 0.f ? 1.f / Le[e] : 0.f;
+        uint16_t* dst = a.out + br * kDV + 64 * w + j;
 #pragma unroll
-        for (int nb = 0; nb < kNB; ++nb)
-          a.out[br * kDV + 16 * nb + j] = (uint16_t)f32_to_bf16_bits(o[rb][nb][e] * inv);
-        if (a.lse && j == 0) {
-          const int qi = row / a.h_q, h = row - qi * a.h_q;
-          a.lse[((size_t)b * a.h_q + h) * a.s_q + qi] =
-              Le[e] > 0.f ? Me[e] * kLn2 + logf(Le[e]) : kNegInf;
-        }
+        for (int nb = 0; nb < kNBw; ++nb)
+          dst[16 * nb] = (uint16_t)f32_to_bf16_bits(o[rb][nb][e] * inv);
       } else {
-        const size_t sx = po.st_base + (size_t)row * po.st_stride;
+        float* dst = a.ws_acc + (po.st_base + (size_t)row * po.st_stride) * kDV + 64 * w + j;
 #pragma unroll
-        for (int nb = 0; nb < kNB; ++nb) a.ws_acc[sx * kDV + 16 * nb + j] = o[rb][nb][e];
-        if (j == 0) {
-          a.ws_m[sx] = Le[e] > 0.f ? Me[e] * kLn2 : kNegInf;  // natural-log units
-          a.ws_l[sx] = Le[e];
-        }
+        for (int nb = 0; nb < kNBw; ++nb) dst[16 * nb] = o[rb][nb][e];
       }
     }
   }
@@ -562,9 +655,8 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t (*tiles)[kTi
 // Fixed splits: workgroup (rg, b, split) takes split `split` of request b,
 // cut at multiples of 32 tokens.
 template <bool kBlockUniform>
-__global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t tiles[kDepth][kTileBytes];
-  __shared__ int restart_vote[kWaves];
+__global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(const MlaArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
   const int b = blockIdx.y, split = blockIdx.z;
   const int s_cap = a.max_blocks * a.block_size;
   const int S = min(max(a.seq_lens[b], 0), s_cap);
@@ -576,7 +668,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_kernel(const MlaArgs a) {
   po.direct = ns == 1;
   po.st_base = (size_t)b * a.R * ns + split;
   po.st_stride = ns;
-  mla_piece<kBlockUniform>(a, tiles, restart_vote, b, blockIdx.x, S, seg_start, seg_end, po);
+  mla_piece<kBlockUniform>(a, smem, b, blockIdx.x, S, seg_start, seg_end, po);
 }
 
 // Log-sum-exp fold of `count` states of one (request, query row), in order,
@@ -705,9 +797,8 @@ __global__ __launch_bounds__(256) void mla_plan_kernel(const MlaArgs a, uint64_t
 
 // Workgroup (w, rg): share w of row group rg.
 template <bool kBlockUniform>
-__global__ __launch_bounds__(256, 1) void mla_decode_balanced_kernel(const MlaArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t tiles[kDepth][kTileBytes];
-  __shared__ int restart_vote[kWaves];
+__global__ __launch_bounds__(kThreads, 1) void mla_decode_balanced_kernel(const MlaArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
   const int w = blockIdx.x, rg = blockIdx.y;
   const int s_cap = a.max_blocks * a.block_size;
   const uint64_t T = a.pre[a.B];
@@ -724,7 +815,7 @@ __global__ __launch_bounds__(256, 1) void mla_decode_balanced_kernel(const MlaAr
     po.direct = t == p0 && t1 == p1;
     po.st_base = (size_t)(2 * w + (t == t0 ? 0 : 1)) * a.R;
     po.st_stride = 1;
-    mla_piece<kBlockUniform>(a, tiles, restart_vote, b, rg, S, (int)(t - p0) * kTile,
+    mla_piece<kBlockUniform>(a, smem, b, rg, S, (int)(t - p0) * kTile,
                              min(S, (int)(t1 - p0) * kTile), po);
     t = t1;
   }
@@ -833,9 +924,9 @@ hipError_t launch_splitkv(const mla::MlaArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)((a.R + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup), a.B,
                   a.num_splits);
   if (a.block_size % mla::kTile == 0)
-    hipLaunchKernelGGL(mla::mla_decode_kernel<true>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mla::mla_decode_kernel<true>, grid, dim3(mla::kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(mla::mla_decode_kernel<false>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mla::mla_decode_kernel<false>, grid, dim3(mla::kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -946,9 +1037,11 @@ extern "C" int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_
   if ((err = hipGetLastError()) != hipSuccess) return err;
   const unsigned rg = (unsigned)((a.R + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup);
   if (block_size % mla::kTile == 0)
-    hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<true>, dim3(n, rg), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<true>, dim3(n, rg), dim3(mla::kThreads), 0,
+                       stream, a);
   else
-    hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<false>, dim3(n, rg), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<false>, dim3(n, rg), dim3(mla::kThreads), 0,
+                       stream, a);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   const size_t rows = (size_t)B * a.R;
   hipLaunchKernelGGL(mla::mla_decode_balanced_merge_kernel, dim3((unsigned)((rows + 3) / 4)),

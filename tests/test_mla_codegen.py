@@ -3,9 +3,10 @@ csrc/mla_decode.hip for gfx950 to assembly).
 
 The kernels' speed rests on properties of the generated code that a compiler
 change or an innocent-looking edit can silently break, so they are checked here:
-  - no scratch (spill) access inside the tile loops: the 256 accumulators fill
-    the accumulation registers, and a spill reload waits for every HBM->LDS
-    copy in flight;
+  - no scratch (spill) access inside the tile loops: with two waves per SIMD a
+    wave has 256 registers, of which the 128 PV accumulators and the 72 Q^T
+    registers take 200, and a spill reload waits for every HBM->LDS copy in
+    flight;
   - no compiler-inserted vmcnt wait inside the tile loops (the copies are
     awaited only by the kernel's own s_waitcnt before each barrier);
   - no compiler use of M0: the copies set M0 in inline assembly, and M0 is a
@@ -42,20 +43,49 @@ def kernel_body(asm, mangled):
     return asm[start:asm.index("s_endpgm", start)]
 
 
+BLOCK_START = re.compile(r"(\.LBB\w+:|; %bb\.\d+:)")
+
+
 def tile_loops(body):
-    """(text of each loop that issues MFMAs, from its header to its first
-    barrier)."""
-    lines = body.split("\n")
-    loops = []
-    for i, ln in enumerate(lines):
-        if "Loop Header" in ln:
-            for k in range(i + 1, len(lines)):
-                if "s_barrier" in lines[k]:
-                    text = "\n".join(lines[i:k])
-                    if "v_mfma" in text:
-                        loops.append(text)
-                    break
-    return loops
+    """(text of each loop that issues MFMAs itself, with the loops nested in
+    it: the blocks the compiler's loop annotations place there, in layout
+    order). A header block is annotated "Loop Header" (and "Parent Loop X" when
+    nested), any other block "in Loop: Header=X"."""
+    blocks = []
+    for ln in body.split("\n"):
+        if BLOCK_START.match(ln) or not blocks:
+            blocks.append([])
+        blocks[-1].append(ln)
+    parent, inner = {}, []
+    for blk in blocks:
+        lab = re.match(r"\.L(BB\w+):", blk[0])
+        notes = []
+        for ln in blk:  # the leading comment lines
+            s = ln.strip()
+            if s and not s.startswith(";") and not BLOCK_START.match(s):
+                break
+            notes.append(s)
+        note = " ".join(notes)
+        if "Loop Header" in note and lab:
+            me = lab.group(1)
+            up = re.search(r"Parent Loop (BB\w+)", note)
+            parent[me] = up.group(1) if up else None
+            inner.append(me)
+        else:
+            m = re.search(r"in Loop: Header=(BB\w+)", note)
+            inner.append(m.group(1) if m else None)
+    def chain(h):
+        out = []
+        while h:
+            out.append(h)
+            h = parent.get(h)
+        return out
+    direct = {h for blk, h in zip(blocks, inner) if h and any("v_mfma" in ln for ln in blk)}
+    # The tile loops: loops issuing MFMAs with no MFMA-issuing loop inside
+    # (a balanced kernel's loop over pieces holds the tile loops).
+    tiles = [h for h in direct if not any(h in chain(d)[1:] for d in direct)]
+    return ["\n".join("\n".join(blk) for blk, h in zip(blocks, inner) if h and top in chain(h))
+            for top in sorted(tiles)]
 
 
 KERNELS = ["_ZN3mla17mla_decode_kernelILb1EEEvNS_7MlaArgsE",
@@ -75,7 +105,9 @@ def test_tile_loops_clean(asm, mangled):
         # not name vmcnt.
         own = re.sub(r";;#ASMSTART.*?(;;#ASMEND|\Z)", "", text, flags=re.S)
         assert "vmcnt" not in own, "compiler vmcnt wait inside a tile loop"
-        assert text.count("v_mfma_f32_16x16x32_bf16") == 136
+        # One interval: QK^T of 16 rows x 32 tokens (36) and PV of 128 rows x
+        # 64 dims (32).
+        assert text.count("v_mfma_f32_16x16x32_bf16") == 68
 
 
 @pytest.mark.parametrize("mangled", KERNELS)
@@ -85,8 +117,9 @@ def test_m0_only_in_inline_asm(asm, mangled):
 
 
 def is_vote_address(line):
-    """The restart votes follow the tile ring (kDepth tiles of ~36 KiB): the only
-    LDS data at byte offsets of 128 KiB and up, added as an immediate."""
+    """The restart votes sit in the second P buffer, after the tile ring (4 tiles
+    of 36 KiB): LDS byte offsets of 128 KiB and up, added to the wave's index
+    as an immediate."""
     m = re.search(r"s_add\w*\s+s\d+,\s*s\d+,\s*0x([0-9a-f]+)", line)
     return bool(m) and int(m.group(1), 16) >= 0x20000
 
@@ -98,7 +131,7 @@ def test_restart_ballot_sees_every_lane(asm, mangled):
     # lane-0 branch narrows the exec mask: inside it, it would see lane 0 only.
     lines = kernel_body(asm, mangled).split("\n")
     stores = [i for i, ln in enumerate(lines)
-              if "ds_write_b32" in ln and any(is_vote_address(p) for p in lines[max(0, i - 4):i])]
+              if "ds_write_b32" in ln and any(is_vote_address(p) for p in lines[max(0, i - 8):i])]
     assert stores, "restart vote store not found"
     for i in stores:
         # The branch narrows exec with s_and_saveexec or by writing exec.
