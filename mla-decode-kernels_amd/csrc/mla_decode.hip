@@ -6,7 +6,7 @@
 // Work decomposition. A workgroup of 8 waves (two per SIMD) owns 128 query
 // rows (a row group) of one request and a range of its tokens. All rows share
 // the cache rows, so each 32-token tile (36 KiB) is read from HBM once per
-// workgroup: the waves copy it cooperatively, HBM -> LDS
+// workgroup: the four PV-first waves copy it, HBM -> LDS
 // (global_load_lds_dwordx4, no registers), into a ring of kDepth slots, and
 // every wave computes from LDS. Two launches share this tile walk (mla_piece):
 //   fixed splits  grid (row groups, B, num_splits), split s of each request;
@@ -109,6 +109,18 @@ static_assert(kDV / kWaves == 64, "wave w accumulates the tile's column block w"
 static_assert(kTileBlocks == 4 * kColBlocks, "a tile is 4 row blocks of 9 column blocks");
 static_assert(kLdsBytes <= 160 * 1024, "the ring and the P buffers fill the LDS");
 static_assert(kWavesHi * 2 <= kWaves, "the waves that take kLoadsHi copies accumulate first");
+#ifndef MLA_COPY_WAVES
+#define MLA_COPY_WAVES 4
+#endif
+// Waves that issue a tile's copies: only the 4 PV-first waves (9 copies
+// each; a copy instruction's issue stalls its wave while the address unit
+// works through the others), which leaves the QK-first waves free to start
+// their QK^T right after the barrier; or (MLA_COPY_WAVES=8) all 8 waves.
+constexpr int kCopyWaves = MLA_COPY_WAVES;
+static_assert(kCopyWaves == 8 || kCopyWaves == 4, "copy waves");
+constexpr int kCopyStride = kCopyWaves / 2;  // copy waves per row-block parity
+constexpr int kCopyHi = kCopyWaves == 8 ? kLoadsHi : kTileBlocks / 4;  // copies of waves < 4
+constexpr int kCopyLo = kCopyWaves == 8 ? kLoadsLo : 0;                // copies of waves >= 4
 
 // Position XOR of row r's 16-byte chunks in a column block of row block rb8
 // (the table depends on rb8's parity; found by a search over tables that
@@ -276,8 +288,9 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
 
   // Copies. Wave w copies row blocks of parity par = w % 2 only (row blocks
   // par and par + 2: 18 column blocks m, rb8 = par + 2 (m / 9), cb = m % 9),
-  // taking m = w / 2 + 4 i (i < 5, m < 18): 5 copies for waves 0-3, 4 for
-  // waves 4-7. Lane x fills row cr = x / 8 of a column block, position x % 8,
+  // taking m = w / 2 + 2 i (i < 9, m < 18): 9 copies for each of waves 0-3,
+  // none for waves 4-7 (with MLA_COPY_WAVES=8: m = w / 2 + 4 i, 5 copies for
+  // waves 0-3, 4 for waves 4-7). Lane x fills row cr = x / 8 of a column block, position x % 8,
   // from that row's chunk (x % 8) ^ chunk_swz(par, cr): one source offset
   // per lane, ro (the row's offset; ro & 0x70 is its chunk's offset in row 0).
   const int par = w & 1, cu = w >> 1;
@@ -365,7 +378,7 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
       const uint16_t* base = a.kv + ((size_t)id * bs + (ts - (int)lb * bs)) * kD;
       const int nvalid = seg_end - ts;
       auto copy = [&](int i) {
-        const int m = cu + 4 * i, hi = m >= kColBlocks ? 1 : 0;
+        const int m = cu + kCopyStride * i, hi = m >= kColBlocks ? 1 : 0;
         const int rb8 = par + 2 * hi, cb = m - kColBlocks * hi;
         // (The row block's offset stays in the lane offset: a row past
         // seg_end must land on the tile's first row, not the block's.)
@@ -374,9 +387,14 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
         load_to_lds(base + 64 * cb, voff,
                     __builtin_amdgcn_readfirstlane(slot + (kColBlocks * rb8 + cb) * 1024));
       };
+      if constexpr (kCopyWaves == 8) {
 #pragma unroll
-      for (int i = 0; i < kLoadsLo; ++i) copy(i);
-      if (w < kWavesHi) copy(kLoadsLo);
+        for (int i = 0; i < kLoadsLo; ++i) copy(i);
+        if (w < kWavesHi) copy(kLoadsLo);
+      } else if (w < kWavesHi) {
+#pragma unroll
+        for (int i = 0; i < kCopyHi; ++i) copy(i);
+      }
     } else {
       // The tile's tokens span blocks lb_lo .. lb_hi: fetch their ids with
       // uniform loads and let each lane take its own rows (one per row block
@@ -402,14 +420,19 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
       for (int x = 0; x < 2; ++x)
         src[x] = a.kv + (row[x] * bs + (ts + tok[x] - lbl[x] * bs)) * kD + ((ro & 0x70u) >> 1);
       auto copy = [&](int i) {
-        const int m = cu + 4 * i, hi = m >= kColBlocks ? 1 : 0;
+        const int m = cu + kCopyStride * i, hi = m >= kColBlocks ? 1 : 0;
         const int rb8 = par + 2 * hi, cb = m - kColBlocks * hi;
         load_to_lds((hi ? src[1] : src[0]) + 64 * cb,
                     __builtin_amdgcn_readfirstlane(slot + (kColBlocks * rb8 + cb) * 1024));
       };
+      if constexpr (kCopyWaves == 8) {
 #pragma unroll
-      for (int i = 0; i < kLoadsLo; ++i) copy(i);
-      if (w < kWavesHi) copy(kLoadsLo);
+        for (int i = 0; i < kLoadsLo; ++i) copy(i);
+        if (w < kWavesHi) copy(kLoadsLo);
+      } else if (w < kWavesHi) {
+#pragma unroll
+        for (int i = 0; i < kCopyHi; ++i) copy(i);
+      }
     }
   };
   // End of an interval: the next tile must have landed (with a refill in
@@ -418,9 +441,9 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
     if (!refill)
       publish_barrier<0>();
     else if (w < kWavesHi)
-      publish_barrier<kLoadsHi>();
+      publish_barrier<kCopyHi>();
     else
-      publish_barrier<kLoadsLo>();
+      publish_barrier<kCopyLo>();
   };
 
   f32x4_t o[kRowBlocks][kNBw];
@@ -560,7 +583,15 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
       if (refill) stage(s + 2, id_next);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (kPV && kPVFirst) accumulate(s - 1);
-      if constexpr (kQK) score(s);
+      if constexpr (kQK) {
+        // The QK-first wave of each SIMD scores at raised issue priority: its
+        // softmax (VALU) then overlaps the other wave's matrix work, instead
+        // of both waves' QK^T contending for the LDS and both softmaxes
+        // leaving the matrix unit idle.
+        if constexpr (!kPVFirst) __builtin_amdgcn_s_setprio(2);
+        score(s);
+        if constexpr (!kPVFirst) __builtin_amdgcn_s_setprio(0);
+      }
       if constexpr (kPV && !kPVFirst) accumulate(s - 1);
       // The block id of the next interval's refill, loaded here so that its
       // latency overlaps the wait below.
