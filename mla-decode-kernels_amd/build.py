@@ -11,6 +11,8 @@ Products (in-tree, git-ignored, shipped with the source tree):
   lib/gqa_decode_ext*.so     g++: host-only torch operator layer linking the above
   lib/libgqa_stream_probe.so hipcc: the streaming-read probe bench.py measures
                              the bandwidth ceiling with (not on the decode path)
+  lib/libissue_probe.so      hipcc: MFMA / VALU / LDS issue-rate probes
+                             (bench/issue_probe.py; not on the decode path)
 
 The extension is compiled as plain C++ (no .cu/.hip source, so torch's
 hipify pass never runs); it reaches the GPU only through the C ABI.
@@ -34,6 +36,7 @@ ARCH = "gfx950"
 
 KERNEL_LIB = os.path.join(LIB_DIR, "libgqa_decode_hip.so")
 PROBE_LIB = os.path.join(LIB_DIR, "libgqa_stream_probe.so")
+ISSUE_PROBE_LIB = os.path.join(LIB_DIR, "libissue_probe.so")
 HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip", "gqa_decode_mfma.hip",
                "gqa_decode_balanced.hip", "mla_decode.hip"]
 # Packed fp32 VALU ops are disabled for all device code.
@@ -70,13 +73,13 @@ def build_kernels(out=KERNEL_LIB, defines=()):
     return out
 
 
-def build_probe():
+def build_probe(src="stream_probe.hip", lib=PROBE_LIB):
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    tmp = PROBE_LIB + ".tmp"
-    dt = _run([hipcc, *HIP_FLAGS, "-shared", os.path.join(CSRC, "stream_probe.hip"), "-o", tmp])
-    os.replace(tmp, PROBE_LIB)
-    print(f"built {os.path.relpath(PROBE_LIB, REPO_ROOT)} in {dt:.1f}s")
-    return PROBE_LIB
+    tmp = lib + ".tmp"
+    dt = _run([hipcc, *HIP_FLAGS, "-shared", os.path.join(CSRC, src), "-o", tmp])
+    os.replace(tmp, lib)
+    print(f"built {os.path.relpath(lib, REPO_ROOT)} in {dt:.1f}s")
+    return lib
 
 
 def ext_filename():
@@ -131,6 +134,7 @@ def main(argv=None):
         return
     build_kernels()
     build_probe()
+    build_probe("issue_probe.hip", ISSUE_PROBE_LIB)
     if not args.no_ext:
         build_extension()
 

@@ -169,6 +169,32 @@ constexpr float kRefSlack = 32.f;
 // kKRing single-read slots (each read kKRing - 1 MFMAs ahead), PV P-operand
 // reads kPAhead row blocks (4 MFMAs each) ahead.
 constexpr int kKRing = 5;
+
+// Profiling build (build.py --variant NAME --define MLA_PHASE_TIMING=1; read
+// by bench/mla_phases.py): every wave stamps the shader clock (s_memtime) at
+// the phase boundaries of its tile intervals and pieces and adds the cycles
+// to its row of mla_phase_cycles (one row per wave of the first 256
+// workgroups; columns kPh*). The stamps wait for the scalar cache, which
+// costs a few percent; the shipped library is built without them.
+#ifndef MLA_PHASE_TIMING
+#define MLA_PHASE_TIMING 0
+#endif
+enum PhaseCol {
+  kPhCopies, kPhFirst, kPhQK, kPhSoftmax, kPhSecond, kPhBarrier, kPhIntervals,  // full intervals
+  kPhQLoad, kPhPrologue, kPhKind0, kPhKind2, kPhVote, kPhEpilogue, kPhPieces,    // pieces
+  kPhKernel, kPhKernelRealtime, kPhCols
+};
+#if MLA_PHASE_TIMING
+__device__ unsigned long long mla_phase_cycles[2048][kPhCols];
+#define MLA_STAMP(x)                                                    \
+  __builtin_amdgcn_sched_barrier(0);                                    \
+  const uint32_t x = (uint32_t)__builtin_amdgcn_s_memtime();           \
+  __builtin_amdgcn_sched_barrier(0)
+#define MLA_PHASE_ADD(col, from, to) (ph[col] += (to) - (from))
+#else
+#define MLA_STAMP(x)
+#define MLA_PHASE_ADD(col, from, to)
+#endif
 constexpr int kPAhead = 2;
 
 // Direct HBM -> LDS copies of 16 bytes per lane (global_load_lds_dwordx4):
@@ -277,6 +303,11 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   // Every lane-dependent value below derives from tid, refreshed here so that
   // none of them is hoisted out of a caller's loop over pieces.
+  MLA_STAMP(ph_start);
+#if MLA_PHASE_TIMING
+  uint32_t ph[kPhCols] = {};
+  uint32_t ph_mid = 0, ph_pro = 0;
+#endif
   uint32_t tid = threadIdx.x;
   refresh(tid);
   const int lane = (int)(tid & 63);
@@ -351,6 +382,8 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
   // the tile loop, where it would also wait for every tile copy in flight.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
+  MLA_STAMP(ph_q);
+  MLA_PHASE_ADD(kPhQLoad, ph_start, ph_q);
   const int* bt = a.block_table + (size_t)b * a.max_blocks;
   // The table is read-only for the launch; through the constant address space
   // the uniform block-id loads become scalar loads.
@@ -484,6 +517,12 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
     // rounded values). The lane's tokens are live iff 16 tg + e < d; a tile
     // where that holds for every lane (d >= 20 everywhere) skips the masking.
     const int d = lim4 - ts;
+#if MLA_PHASE_TIMING
+    {
+      MLA_STAMP(ph_m);
+      ph_mid = ph_m;
+    }
+#endif
     const bool partial = __builtin_amdgcn_ballot_w64(d < 20) != 0;
     float sc[2][4];
     float mx = kNegInf;
@@ -579,10 +618,13 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
       refresh(qoff);
       refresh(vx0);
       refresh(vx1);
+      MLA_STAMP(ph0);
       const bool refill = kQK && s + 2 < ntiles;
       if (refill) stage(s + 2, id_next);
       __builtin_amdgcn_sched_barrier(0);
+      MLA_STAMP(ph1);
       if constexpr (kPV && kPVFirst) accumulate(s - 1);
+      MLA_STAMP(ph2);
       if constexpr (kQK) {
         // The QK-first wave of each SIMD scores at raised issue priority: its
         // softmax (VALU) then overlaps the other wave's matrix work, instead
@@ -592,13 +634,31 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
         score(s);
         if constexpr (!kPVFirst) __builtin_amdgcn_s_setprio(0);
       }
+      MLA_STAMP(ph3);
       if constexpr (kPV && !kPVFirst) accumulate(s - 1);
       // The block id of the next interval's refill, loaded here so that its
       // latency overlaps the wait below.
       if constexpr (kBlockUniform) {
         if (s + 3 < ntiles) id_next = block_id(s + 3);
       }
+      MLA_STAMP(ph4);
       publish(refill);
+      MLA_STAMP(ph5);
+#if MLA_PHASE_TIMING
+      if constexpr (kKind == 1) {
+        MLA_PHASE_ADD(kPhCopies, ph0, ph1);
+        MLA_PHASE_ADD(kPhFirst, ph1, ph2);
+        MLA_PHASE_ADD(kPhQK, ph2, ph_mid);
+        MLA_PHASE_ADD(kPhSoftmax, ph_mid, ph3);
+        MLA_PHASE_ADD(kPhSecond, ph3, ph4);
+        MLA_PHASE_ADD(kPhBarrier, ph4, ph5);
+        ph[kPhIntervals] += 1;
+      } else if constexpr (kKind == 0) {
+        MLA_PHASE_ADD(kPhKind0, ph0, ph5);
+      } else {
+        MLA_PHASE_ADD(kPhKind2, ph0, ph5);
+      }
+#endif
     };
     // Prologue: tiles 0 and 1 in flight; tile 0 published.
     stage(0, kBlockUniform ? block_id(0) : 0);
@@ -607,6 +667,12 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
       if (ntiles > 2) id_next = block_id(2);
     }
     publish(ntiles > 1);
+#if MLA_PHASE_TIMING
+    {
+      MLA_STAMP(ph_p);
+      ph_pro = ph_p;
+    }
+#endif
     interval(std::integral_constant<int, 0>{}, 0);
     for (int s = 1; s < ntiles; ++s) interval(std::integral_constant<int, 1>{}, s);
     interval(std::integral_constant<int, 2>{}, ntiles);
@@ -619,6 +685,8 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
   };
 
   run_pass();
+  MLA_STAMP(ph_run);
+  MLA_PHASE_ADD(kPhPrologue, ph_q, ph_pro);
   // A row whose max beat its reference by more than kRefSlack has overflowed
   // or lost precision: the workgroup (which stages tiles together) runs the
   // split again with every row's reference at its true max (probabilities
@@ -636,6 +704,8 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
     run_pass();
   }
 
+  MLA_STAMP(ph_vote);
+  MLA_PHASE_ADD(kPhVote, ph_run, ph_vote);
   // Row j's final l (lane (j, g) holds l over its own tokens), published to
   // every wave through the LDS; its owner writes the row's (m, l) or lse.
   float L = lsum + __shfl_xor(lsum, 16, 64);
@@ -681,6 +751,15 @@ __device__ __forceinline__ void mla_piece(const MlaArgs& a, uint8_t* smem, int b
       }
     }
   }
+#if MLA_PHASE_TIMING
+  MLA_STAMP(ph_end);
+  MLA_PHASE_ADD(kPhEpilogue, ph_vote, ph_end);
+  ph[kPhPieces] += 1;
+  if (lane == 0 && blockIdx.x + gridDim.x * blockIdx.y < 256) {
+    unsigned long long* row = mla_phase_cycles[(blockIdx.x + gridDim.x * blockIdx.y) * kWaves + w];
+    for (int c = 0; c < kPhKernel; ++c) atomicAdd(row + c, (unsigned long long)ph[c]);
+  }
+#endif
 }
 
 // Fixed splits: workgroup (rg, b, split) takes split `split` of request b,
@@ -837,6 +916,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_balanced_kernel(const 
   if (w >= n) return;
   const uint64_t t0 = share_start(T, w, n), t_end = share_start(T, w + 1, n);
   int b = a.first[w];
+#if MLA_PHASE_TIMING
+  const uint64_t k_t0 = __builtin_amdgcn_s_memtime(), k_r0 = __builtin_amdgcn_s_memrealtime();
+#endif
   for (uint64_t t = t0; t < t_end; ++b) {
     const uint64_t p0 = a.pre[b], p1 = a.pre[b + 1];
     if (p1 <= t) continue;  // a request with no tiles
@@ -850,6 +932,14 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_balanced_kernel(const 
                              min(S, (int)(t1 - p0) * kTile), po);
     t = t1;
   }
+#if MLA_PHASE_TIMING
+  const uint64_t k_t1 = __builtin_amdgcn_s_memtime(), k_r1 = __builtin_amdgcn_s_memrealtime();
+  if ((threadIdx.x & 63) == 0 && w + gridDim.x * rg < 256) {
+    unsigned long long* row = mla_phase_cycles[(w + gridDim.x * rg) * kWaves + (threadIdx.x >> 6)];
+    atomicAdd(row + kPhKernel, (unsigned long long)(k_t1 - k_t0));
+    atomicAdd(row + kPhKernelRealtime, (unsigned long long)(k_r1 - k_r0));
+  }
+#endif
 }
 
 // Rows of requests cut by share boundaries: fold their pieces in share order
@@ -1080,3 +1170,16 @@ extern "C" int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_
   return hipGetLastError();
 }
 
+
+#if MLA_PHASE_TIMING
+// Profiling build only (not part of include/mla_decode.h): copies the phase
+// cycle table (2048 x kPhCols uint64, see mla_phase_cycles) to host memory,
+// or with reset != 0 zeroes it first. Returns a hipError_t code.
+extern "C" __attribute__((visibility("default"))) int mla_decode_phase_table(void* host,
+                                                                            int reset) {
+  static unsigned long long zero[2048][mla::kPhCols];
+  if (reset)
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(mla::mla_phase_cycles), zero, sizeof(zero));
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(mla::mla_phase_cycles), sizeof(zero));
+}
+#endif

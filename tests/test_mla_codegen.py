@@ -164,3 +164,24 @@ def test_row_max_uses_both_swap_results(llvm_ir):
     for v in calls:
         assert re.search(rf"extractvalue \{{ i32, i32 \}} {re.escape(v)}, 1\b", llvm_ir), \
             f"second result of {v} unused"
+
+
+def test_phase_timing_build_keeps_tile_loops_clean(tmp_path):
+    # The profiling build (MLA_PHASE_TIMING, read by bench/mla_phases.py) adds
+    # shader-clock stamps to the tile loops; its numbers describe the shipped
+    # kernel only if the stamps add no spills there.
+    out = tmp_path / "mla_phase.s"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang",
+                    "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                    "-DMLA_PHASE_TIMING=1", f"-I{os.path.join(ROOT, 'include')}",
+                    f"-I{os.path.join(ROOT, 'mla-decode-kernels_amd', 'csrc')}", SRC, "-o",
+                    str(out)], check=True, capture_output=True)
+    text = out.read_text()
+    assert "mla_decode_phase_table" in text
+    for mangled in KERNELS:
+        loops = tile_loops(kernel_body(text, mangled))
+        assert loops
+        for loop in loops:
+            assert "s_memtime" in loop
+            code = [ln for ln in loop.split("\n") if ln.strip() and not ln.strip().startswith(";")]
+            assert not [ln for ln in code if "scratch_" in ln]
