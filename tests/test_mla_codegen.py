@@ -177,7 +177,7 @@ def test_phase_timing_build_keeps_tile_loops_clean(tmp_path):
                     f"-I{os.path.join(ROOT, 'mla-decode-kernels_amd', 'csrc')}", SRC, "-o",
                     str(out)], check=True, capture_output=True)
     text = out.read_text()
-    assert "mla_decode_phase_table" in text
+    assert "mla_phase_cycles" in text
     for mangled in KERNELS:
         loops = tile_loops(kernel_body(text, mangled))
         assert loops
