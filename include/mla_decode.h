@@ -92,12 +92,13 @@ GQA_DECODE_API int mla_decode_combine_launch(void* workspace, size_t workspace_b
  * tiles in request order (T = sum_b ceil(S_b / 32)); each of the ceil(s_q h_q
  * / 128) row groups gets n = num_workgroups / row groups shares
  * (num_workgroups <= 0: the device's CU count), share w taking tiles
- * [w T / n, (w + 1) T / n). Three launches on `stream`: a one-workgroup plan
- * kernel (tile prefix sums and each share's first request, from seq_lens on
- * the device: no host synchronisation, graph-capturable), the split kernel
- * (requests that fall inside one share are written to out and lse directly,
- * the pieces of the others to workspace states), and a merge of the cut
- * requests in share order (bitwise reproducible for a given num_workgroups).
+ * [w T / n, (w + 1) T / n). Two launches on `stream`: the split kernel, each
+ * of whose workgroups plans the launch from seq_lens on the device (tile
+ * prefix sums, its share and first request: no host synchronisation,
+ * graph-capturable; requests that fall inside one share are written to out
+ * and lse directly, the pieces of the others to workspace states), and a
+ * merge of the cut requests in share order (bitwise reproducible for a given
+ * num_workgroups).
  * workspace: mla_decode_balanced_workspace_bytes(B, s_q, h_q, num_workgroups)
  * bytes, 16-byte aligned, uninitialised is fine. */
 GQA_DECODE_API int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_cache,
@@ -108,8 +109,8 @@ GQA_DECODE_API int mla_decode_balanced_launch(const uint16_t* q, const uint16_t*
                                               size_t workspace_bytes, hipStream_t stream);
 
 /* Workspace bytes for mla_decode_balanced_launch (0 for invalid arguments):
- * two states of s_q * h_q rows x (512 + 2) floats per share, the tile prefix
- * sums (B + 2 uint64) and the shares' first requests. */
+ * two states of s_q * h_q rows x (512 + 2) floats per share, then the tile
+ * prefix sums (B + 2 uint64). */
 GQA_DECODE_API size_t mla_decode_balanced_workspace_bytes(int B, int s_q, int h_q,
                                                           int num_workgroups);
 

@@ -11,9 +11,10 @@
 // every wave computes from LDS. Two launches share this tile walk (mla_piece):
 //   fixed splits  grid (row groups, B, num_splits), split s of each request;
 //   balanced      one workgroup per CU and row group, each taking an equal
-//                 share of the batch's request-ordered tiles (a plan kernel
-//                 computes the tile prefix sums on the device), walked piece
-//                 by piece; requests cut between shares are merged after.
+//                 share of the batch's request-ordered tiles (each
+//                 workgroup plans its share from seq_lens on the device),
+//                 walked piece by piece; requests cut between shares are
+//                 merged after.
 //
 // The two matrix products of a tile are split between the waves along
 // different axes, which keeps each wave's registers at what two waves per
@@ -144,8 +145,7 @@ struct MlaArgs {
   float* ws_acc;  // [B, R, ns, 512]
   float* ws_m;    // [B, R, ns] natural-log units
   float* ws_l;
-  const uint64_t* pre;  // balanced launch: tile prefix sums [B + 1]
-  const int* first;     // balanced launch: each share's first request
+  uint64_t* pre;        // balanced launch: tile prefix sums [B + 2] (written by the split kernel)
   int B, s_q, h_q, R, block_size, max_blocks, num_splits, causal, nshare;
   FastDiv bs_div;
   float scale_log2e;
@@ -858,70 +858,74 @@ __device__ __forceinline__ uint64_t share_start(uint64_t T, int w, int n) {
   return (uint64_t)w * T / (uint64_t)n;
 }
 
-// Tile prefix sums pre[b] = sum_{b' < b} ceil(S_b' / 32) (b = 0..B, S clamped
-// to the block table), the working share count pre[B + 1] = min(nshare, T),
-// and each working share's first request (the first b with pre[b + 1] > its
-// first tile); one workgroup.
-__global__ __launch_bounds__(256) void mla_plan_kernel(const MlaArgs a, uint64_t* pre, int* first) {
-  __shared__ uint64_t part[256];
-  const int tid = threadIdx.x;
-  const int per = (a.B + 255) / 256;
-  const int b0 = min(tid * per, a.B), b1 = min(b0 + per, a.B);
-  const int s_cap = a.max_blocks * a.block_size;
-  auto tiles_of = [&](int b) -> uint64_t {
-    const int S = min(max(a.seq_lens[b], 0), s_cap);
-    return (uint64_t)((S + kTile - 1) / kTile);
-  };
-  uint64_t sum = 0;
-  for (int b = b0; b < b1; ++b) sum += tiles_of(b);
-  part[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan of the 256 partial sums
-    const uint64_t v = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
-  }
-  uint64_t run = part[tid] - sum;
-  for (int b = b0; b < b1; ++b) {
-    pre[b] = run;
-    run += tiles_of(b);
-  }
-  const uint64_t T = part[255];
-  const int n = (int)(T < (uint64_t)a.nshare ? T : (uint64_t)a.nshare);
-  if (tid == 0) {
-    pre[a.B] = T;
-    pre[a.B + 1] = (uint64_t)n;
-  }
-  __syncthreads();  // the prefix sums, written by all threads, are read below
-  for (int w = tid; w < n; w += 256) {
-    const uint64_t t = share_start(T, w, n);
-    int lo = 0, hi = a.B - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (pre[mid + 1] > t) hi = mid; else lo = mid + 1;
-    }
-    first[w] = lo;
-  }
-}
-
-// Workgroup (w, rg): share w of row group rg.
+// Workgroup (w, rg): share w of row group rg. Every workgroup first plans
+// the launch itself from seq_lens (no separate plan launch): the tile counts'
+// inclusive prefix sums over chunks of the batch (one chunk per thread, a
+// scan in P buffer 1, which the first piece does not touch before its
+// second barrier) give T, the working share count n = min(nshare, T), the
+// share's tiles and its first request. Workgroup (0, 0) also writes the
+// request prefix sums pre[b] (b = 0..B), pre[B] = T and pre[B + 1] = n for
+// the merge kernel, before any workgroup can return.
 template <bool kBlockUniform>
 __global__ __launch_bounds__(kThreads, 1) void mla_decode_balanced_kernel(const MlaArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kLdsBytes];
   const int w = blockIdx.x, rg = blockIdx.y;
   const int s_cap = a.max_blocks * a.block_size;
-  const uint64_t T = a.pre[a.B];
-  const int n = (int)a.pre[a.B + 1];
+  auto tiles_of = [&](int b) -> uint64_t {
+    const int S = min(max(a.seq_lens[b], 0), s_cap);
+    return (uint64_t)((S + kTile - 1) / kTile);
+  };
+  uint64_t* const part = reinterpret_cast<uint64_t*>(smem + kDepth * kTileBytes + kPBytes);
+  const int tid = threadIdx.x;
+  const int per = (a.B + kThreads - 1) / kThreads;
+  const int b0 = min(tid * per, a.B), b1 = min(b0 + per, a.B);
+  uint64_t sum = 0;
+  for (int b = b0; b < b1; ++b) sum += tiles_of(b);
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kThreads; off <<= 1) {  // inclusive scan of the chunk sums
+    const uint64_t v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  const uint64_t T = part[kThreads - 1];
+  const int n = (int)(T < (uint64_t)a.nshare ? T : (uint64_t)a.nshare);
+  if (w == 0 && rg == 0) {
+    uint64_t run = part[tid] - sum;
+    for (int b = b0; b < b1; ++b) {
+      a.pre[b] = run;
+      run += tiles_of(b);
+    }
+    if (tid == 0) {
+      a.pre[a.B] = T;
+      a.pre[a.B + 1] = (uint64_t)n;
+    }
+  }
   if (w >= n) return;
   const uint64_t t0 = share_start(T, w, n), t_end = share_start(T, w + 1, n);
-  int b = a.first[w];
+  // The share's first request: the first b whose tiles end past t0 (the
+  // chunk first, by bisection of the chunk prefix sums, then within it).
+  int lo = 0, hi = kThreads - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (part[mid] > t0) hi = mid; else lo = mid + 1;
+  }
+  uint64_t p0 = lo > 0 ? part[lo - 1] : 0;  // tiles before request b
+  int b = lo * per;
+  for (uint64_t nt = tiles_of(b); p0 + nt <= t0; nt = tiles_of(b)) {
+    p0 += nt;
+    ++b;
+  }
 #if MLA_PHASE_TIMING
   const uint64_t k_t0 = __builtin_amdgcn_s_memtime(), k_r0 = __builtin_amdgcn_s_memrealtime();
 #endif
   for (uint64_t t = t0; t < t_end; ++b) {
-    const uint64_t p0 = a.pre[b], p1 = a.pre[b + 1];
-    if (p1 <= t) continue;  // a request with no tiles
+    const uint64_t p1 = p0 + tiles_of(b);
+    if (p1 <= t) {  // a request with no tiles
+      p0 = p1;
+      continue;
+    }
     const uint64_t t1 = p1 < t_end ? p1 : t_end;
     const int S = min(max(a.seq_lens[b], 0), s_cap);
     PieceOut po;
@@ -931,6 +935,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_balanced_kernel(const 
     mla_piece<kBlockUniform>(a, smem, b, rg, S, (int)(t - p0) * kTile,
                              min(S, (int)(t1 - p0) * kTile), po);
     t = t1;
+    p0 = p1;
   }
 #if MLA_PHASE_TIMING
   const uint64_t k_t1 = __builtin_amdgcn_s_memtime(), k_r1 = __builtin_amdgcn_s_memrealtime();
@@ -1018,7 +1023,6 @@ hipError_t make_args(mla::MlaArgs* a, const uint16_t* q, const uint16_t* kv_cach
   a->lse = lse;
   a->ws_acc = a->ws_m = a->ws_l = nullptr;
   a->pre = nullptr;
-  a->first = nullptr;
   a->nshare = 0;
   a->s_q = s_q;
   a->h_q = h_q;
@@ -1126,8 +1130,7 @@ extern "C" size_t mla_decode_balanced_workspace_bytes(int B, int s_q, int h_q, i
   const int n = balanced_shares(s_q, h_q, num_workgroups);
   if (n <= 0) return 0;
   const size_t states = (size_t)2 * n * s_q * h_q;
-  return align16(states * (mla::kDV + 2) * sizeof(float)) + align16((size_t)(B + 2) * 8) +
-         (size_t)n * sizeof(int);
+  return align16(states * (mla::kDV + 2) * sizeof(float)) + (size_t)(B + 2) * 8;
 }
 
 extern "C" int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_cache,
@@ -1149,13 +1152,8 @@ extern "C" int mla_decode_balanced_launch(const uint16_t* q, const uint16_t* kv_
   a.ws_acc = reinterpret_cast<float*>(ws);
   a.ws_m = a.ws_acc + states * mla::kDV;
   a.ws_l = a.ws_m + states;
-  uint64_t* pre = reinterpret_cast<uint64_t*>(ws + align16(states * (mla::kDV + 2) * sizeof(float)));
-  int* first = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(pre) + align16((size_t)(B + 2) * 8));
-  a.pre = pre;
-  a.first = first;
+  a.pre = reinterpret_cast<uint64_t*>(ws + align16(states * (mla::kDV + 2) * sizeof(float)));
   a.nshare = n;
-  hipLaunchKernelGGL(mla::mla_plan_kernel, dim3(1), dim3(256), 0, stream, a, pre, first);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
   const unsigned rg = (unsigned)((a.R + mla::kRowsPerGroup - 1) / mla::kRowsPerGroup);
   if (block_size % mla::kTile == 0)
     hipLaunchKernelGGL(mla::mla_decode_balanced_kernel<true>, dim3(n, rg), dim3(mla::kThreads), 0,

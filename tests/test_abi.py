@@ -416,7 +416,7 @@ def test_mla_balanced_workspace_bytes(B, s_q, h_q, nwg):
     n = max(1, nwg // ((R + 127) // 128))
     states = 2 * n * R
     a16 = lambda x: (x + 15) // 16 * 16  # noqa: E731
-    want = a16(states * 514 * 4) + a16((B + 2) * 8) + n * 4
+    want = a16(states * 514 * 4) + (B + 2) * 8
     assert capi.mla_balanced_workspace_bytes(B, s_q, h_q, nwg) == want
     assert capi.mla_balanced_workspace_bytes(0, s_q, h_q, nwg) == 0
 

@@ -388,8 +388,8 @@ def test_balanced_graph_replay(gpu):
 
 
 def test_balanced_many_requests(gpu):
-    # 3000 short requests (the plan kernel's scan then takes several requests
-    # per thread), checked on a subset.
+    # 3000 short requests (the split kernel's planning scan then takes several
+    # requests per thread), checked on a subset.
     S_list = [(7 * i) % 97 for i in range(3000)]
     case = make_mla_case(S_list, 1, 16, 16, pool_factor=1.0, seed=13, device="cuda")
     got = run_balanced(case, False, 256)

@@ -39,8 +39,10 @@ def asm(tmp_path_factory):
 
 
 def kernel_body(asm, mangled):
+    """The kernel's code: from its label to its end-of-function label (a
+    kernel may end its waves early, so it can hold several s_endpgm)."""
     start = asm.index(f"\n{mangled}:")
-    return asm[start:asm.index("s_endpgm", start)]
+    return asm[start:asm.index("\n.Lfunc_end", start)]
 
 
 BLOCK_START = re.compile(r"(\.LBB\w+:|; %bb\.\d+:)")
