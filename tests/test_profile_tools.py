@@ -105,3 +105,43 @@ def test_stall_breakdown_and_occupancy(tmp_path):
     assert limiter in ("LDS", "grid")
     text, _ = pc.summarize(root)
     assert "dependency wait 70%" in text and "| 96 | 90112 | 4 |" in text
+
+
+@pytest.mark.gpu
+def test_issue_probe_rates(gpu, capsys):
+    # The committed issue-rate probes behind the MLA kernel's wave layout run
+    # and give physically sensible rates: eight MFMA chains near the dense
+    # bf16 peak, and two waves per SIMD hiding FMAs under the matrix unit
+    # better than one wave does.
+    import issue_probe
+
+    assert issue_probe.main(["--iters", "4000"]) == 0
+    out = capsys.readouterr().out
+    rows = {}
+    for ln in out.splitlines():
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        if len(cells) == 7 and cells[0] in ("mfma", "valu", "mfma + valu"):
+            rows[(cells[0], int(cells[1]), int(cells[2]), int(cells[3]))] = float(cells[4])
+    assert ("mfma", 1, 8, 0) in rows and ("mfma + valu", 2, 4, 8) in rows
+    ns_per_mfma = rows[("mfma", 1, 8, 0)] / 8
+    assert 5.0 < ns_per_mfma < 20.0  # 16 cycles at 0.8..3.2 GHz
+    one = rows[("mfma + valu", 1, 4, 8)] / rows[("mfma", 1, 4, 0)]
+    two = rows[("mfma + valu", 2, 4, 8)] / rows[("mfma", 2, 4, 0)]
+    assert two < one
+    assert "ds_read_b128" in out
+
+
+@pytest.mark.gpu
+def test_mla_phase_table(gpu, capsys):
+    # The phase table of the MLA_PHASE_TIMING build (when it has been built:
+    # build.py --variant phase --define MLA_PHASE_TIMING=1) accounts for the
+    # whole kernel: phases within a few percent of the wave's cycles.
+    lib = os.path.join(os.path.dirname(pc.HERE), "_build", "phase", "libgqa_decode_hip.so")
+    if not os.path.exists(lib):
+        pytest.skip("profiling build not present (build.py --variant phase --define MLA_PHASE_TIMING=1)")
+    import mla_phases
+
+    assert mla_phases.main(["--config", "mla_4k", "--steps", "3"]) == 0
+    out = capsys.readouterr().out
+    assert "Cycles per full interval and wave" in out
+    assert "| PV-first 0-3 |" in out and "| QK-first 4-7 |" in out
