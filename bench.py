@@ -474,7 +474,12 @@ def stream_probe(torch, cases, dev):
     request), as the VALU scan runs config 2 at one split), whole-slot reads
     (4 waves per (request, split), 8 splits) and a plain linear read of both
     buffers (256 workgroups of 4 waves), each with non-temporal and plain
-    loads. Events around each launch, median of 20 after 5 warmup launches."""
+    loads. Events around each launch, median of 20 after 5 warmup launches.
+    Then the timed launches (non-temporal): the head-strided gather and a
+    dynamic one (256 persistent workgroups claiming items of 512 or 1024 token
+    slots of one (request, kv-head)), with each workgroup's end time on the
+    GPU's 100 MHz real-time counter (from the launch's first start, last of
+    the 20 timed launches): how much of a launch is its tail."""
     import ctypes
 
     path = os.path.join(PKG_DIR, "lib", "libgqa_stream_probe.so")
@@ -507,6 +512,31 @@ def stream_probe(torch, cases, dev):
                         "tbps": round(2 * nbytes / ms / 1e9, 3),
                         "frac_of_8tbps": round(2 * nbytes / ms / 1e9 / 8.0, 4)}
             log(f"stream probe {key}: {ms * 1e3:.2f} us, {2 * nbytes / ms / 1e9:.3f} TB/s")
+    L.gqa_stream_probe_timed_launch.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [
+        ctypes.c_void_p]
+    L.gqa_stream_probe_timed_launch.restype = ctypes.c_int
+    times = torch.zeros(2 * max(8 * requests, 256), dtype=torch.int64, device=dev)
+    ctr = torch.zeros(2, dtype=torch.int32, device=dev)
+    for pattern, pname, chunk in ((0, "timed_head_strided", 0), (3, "dynamic_512", 512),
+                                  (3, "dynamic_1024", 1024)):
+        def launch():
+            rc = L.gqa_stream_probe_timed_launch(k.data_ptr(), v.data_ptr(), sink.data_ptr(),
+                                                 times.data_ptr(), ctr.data_ptr(), pattern,
+                                                 requests, slots, chunk, sp)
+            if rc != 0:
+                raise RuntimeError(f"gqa_stream_probe_timed_launch returned {rc}")
+        ms = cases.time_op(launch, warmup=5, runs=20)
+        nwg = 8 * requests if pattern == 0 else 256
+        t = times[:2 * nwg].view(nwg, 2).cpu().double()
+        ends = sorted(((t[:, 1] - t[:, 0].min()) * 0.01).tolist())  # 100 MHz ticks -> us
+        q = lambda f: round(ends[min(int(f * nwg), nwg - 1)], 2)  # noqa: E731
+        res[pname] = {"median_us": round(ms * 1e3, 2), "tbps": round(2 * nbytes / ms / 1e9, 3),
+                      "wg_end_us": {"min": round(ends[0], 2), "p10": q(0.1), "p50": q(0.5),
+                                    "p90": q(0.9), "max": round(ends[-1], 2)}}
+        log(f"stream probe {pname}: {ms * 1e3:.2f} us; workgroup ends (us) min {ends[0]:.1f} "
+            f"p50 {q(0.5)} max {ends[-1]:.1f}")
+    if int(ctr.abs().sum()) != 0:
+        raise RuntimeError("dynamic probe left its counters non-zero")
     print(json.dumps({"stream_probe": "config 2 cache, 1 GiB K+V, identity block table",
                       "bytes": 2 * nbytes, "results": res, "clocks": cases.gpu_clocks()}),
           flush=True)

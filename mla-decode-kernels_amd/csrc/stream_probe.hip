@@ -24,6 +24,17 @@
 //                 sequential read, with no gather at all.
 // Each lane folds what it loaded into one word written to `sink`, so no load
 // is dead.
+//
+// The timed entry point (gqa_stream_probe_timed_launch) also records, per
+// workgroup, the 100 MHz real-time counter at its start and end, which shows
+// how much of a launch is its tail; it runs the head-strided pattern or a
+// dynamic one:
+//   dynamic       256 persistent workgroups x 4 waves; the items are
+//                 (chunk, request, kv-head) triples of `chunk` slots, in
+//                 chunk-major order (the first 256 are the head-strided
+//                 pattern's workgroups' first chunks); workgroup g reads item g
+//                 and then claims further items from a counter (a vector
+//                 atomic by thread 0, one item ahead) until none are left.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -73,9 +84,23 @@ __device__ __forceinline__ int round_robin_count(int ntiles, int ph) {
   return ntiles > ph ? (ntiles - ph + 3) / 4 : 0;
 }
 
+// The workgroup's start and end on the 100 MHz real-time counter, by thread 0
+// after a barrier (every wave's loads have been folded by then).
+__device__ __forceinline__ void record_times(unsigned long long* times, int wg,
+                                             unsigned long long t0) {
+  if (times == nullptr) return;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    times[2 * wg] = t0;
+    times[2 * wg + 1] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+
 template <bool kNT>
 __global__ __launch_bounds__(256) void probe_head_strided(const uint8_t* K, const uint8_t* V,
-                                                          uint32_t* sink, int slots) {
+                                                          uint32_t* sink, int slots,
+                                                          unsigned long long* times) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   const int h = blockIdx.x ^ 1, b = blockIdx.y;
   const int lane = threadIdx.x & 63, ph = threadIdx.x >> 6;
   const int r = lane >> 4, c = lane & 15;
@@ -87,6 +112,52 @@ __global__ __launch_bounds__(256) void probe_head_strided(const uint8_t* K, cons
     return (uint32_t)(16 * (ph + 4 * k) + 4 * i + r) * kSlotBytes + h * kRowBytes + 16 * c;
   });
   sink[((size_t)b * gridDim.x + blockIdx.x) * 256 + threadIdx.x] = acc;
+  record_times(times, b * gridDim.x + blockIdx.x, t0);
+}
+
+// Dynamic: `requests` x 8 x (slots / chunk) items of `chunk` slots (see the
+// file comment); ctr[0] counts claims and ctr[1] departures, both zero on
+// entry; the last workgroup to leave sets them back to zero.
+__global__ __launch_bounds__(256) void probe_dynamic(const uint8_t* K, const uint8_t* V,
+                                                     uint32_t* sink, int requests, int slots,
+                                                     int chunk, unsigned int* ctr,
+                                                     unsigned long long* times) {
+  __shared__ int next_item[2];
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  const int lane = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int r = lane >> 4, c = lane & 15;
+  const int per_chunk = requests * kHeads, nitems = per_chunk * (slots / chunk);
+  uint32_t acc = 0;
+  int item = blockIdx.x, par = 0;
+  while (item < nitems) {
+    int claimed = 0;
+    if (threadIdx.x == 0)
+      claimed = (int)__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+                (int)gridDim.x;
+    const int ck = item / per_chunk, bh = item - ck * per_chunk;
+    const int b = bh / kHeads, h = (bh % kHeads) ^ 1;
+    const size_t base = ((size_t)b * slots + (size_t)ck * chunk) * kSlotBytes;
+    const uint32_t bytes = (uint32_t)chunk * kSlotBytes;
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(K + base), 0, bytes, 0x00020000);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)(V + base), 0, bytes, 0x00020000);
+    acc += stream_tiles<true>(rk, rv, round_robin_count(chunk / 16, ph), [&](int k, int i) {
+      return (uint32_t)(16 * (ph + 4 * k) + 4 * i + r) * kSlotBytes + h * kRowBytes + 16 * c;
+    });
+    if (threadIdx.x == 0) next_item[par] = claimed;
+    __syncthreads();
+    item = next_item[par];
+    par ^= 1;
+  }
+  sink[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
+  record_times(times, blockIdx.x, t0);
+  if (threadIdx.x == 0) {
+    const uint32_t left = __hip_atomic_fetch_add(ctr + 1, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if (left == gridDim.x - 1) {
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 template <bool kNT>
@@ -141,9 +212,11 @@ extern "C" __attribute__((visibility("default"))) int gqa_stream_probe_launch(
   if (pattern == 0) {
     const dim3 grid(kHeads, requests);
     if (nontemporal)
-      hipLaunchKernelGGL(probe_head_strided<true>, grid, dim3(256), 0, stream, K, V, sink, slots);
+      hipLaunchKernelGGL(probe_head_strided<true>, grid, dim3(256), 0, stream, K, V, sink, slots,
+                         nullptr);
     else
-      hipLaunchKernelGGL(probe_head_strided<false>, grid, dim3(256), 0, stream, K, V, sink, slots);
+      hipLaunchKernelGGL(probe_head_strided<false>, grid, dim3(256), 0, stream, K, V, sink, slots,
+                         nullptr);
   } else if (pattern == 1) {
     if (splits < 1 || splits > 65535 || slots % (2 * splits) != 0) return hipErrorInvalidValue;
     const dim3 grid(splits, requests);
@@ -160,6 +233,35 @@ extern "C" __attribute__((visibility("default"))) int gqa_stream_probe_launch(
     else
       hipLaunchKernelGGL(probe_linear<false>, dim3(splits), dim3(256), 0, stream, K, V, sink,
                          (uint32_t)bytes);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Timed runs (non-temporal loads): pattern 0 head-strided (grid 8 x requests),
+// pattern 3 dynamic (256 workgroups, items of `chunk` slots). times receives
+// (start, end) per workgroup on the 100 MHz real-time counter: 8 * requests
+// pairs for pattern 0, 256 for pattern 3. ctr (pattern 3): two 32-bit
+// counters, zero before the first launch and left zero by each. sink: one word
+// per thread (8 * requests * 256 words suffice for both). Same size rules as
+// above; pattern 3 also needs 16 <= chunk, slots % chunk == 0 and chunk % 16 == 0.
+extern "C" __attribute__((visibility("default"))) int gqa_stream_probe_timed_launch(
+    const void* k, const void* v, uint32_t* sink, unsigned long long* times, unsigned int* ctr,
+    int pattern, int requests, int slots, int chunk, hipStream_t stream) {
+  if (!k || !v || !sink || !times || requests < 1 || requests > 65535 || slots < 64 ||
+      slots % 64 != 0 || (uint64_t)slots * kSlotBytes >= (uint64_t(1) << 32))
+    return hipErrorInvalidValue;
+  const auto* K = static_cast<const uint8_t*>(k);
+  const auto* V = static_cast<const uint8_t*>(v);
+  if (pattern == 0) {
+    hipLaunchKernelGGL(probe_head_strided<true>, dim3(kHeads, requests), dim3(256), 0, stream, K,
+                       V, sink, slots, times);
+  } else if (pattern == 3) {
+    if (!ctr || chunk < 16 || chunk % 16 != 0 || slots % chunk != 0 || requests * kHeads < 256)
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL(probe_dynamic, dim3(256), dim3(256), 0, stream, K, V, sink, requests, slots,
+                       chunk, ctr, times);
   } else {
     return hipErrorInvalidValue;
   }

@@ -145,3 +145,26 @@ def test_mla_phase_table(gpu, capsys):
     out = capsys.readouterr().out
     assert "Cycles per full interval and wave" in out
     assert "| PV-first 0-3 |" in out and "| QK-first 4-7 |" in out
+
+
+@pytest.mark.gpu
+def test_stream_probe_patterns(gpu, capsys):
+    # bench.py --stream-probe: every pattern reads config 2's 1 GiB of K and V
+    # at a physical rate; the timed patterns record every workgroup's end (in
+    # order: first <= median <= last, the last within the launch); the dynamic
+    # pattern leaves its claim counters at zero (stream_probe checks that).
+    import torch
+
+    import bench
+    import cases
+
+    assert bench.stream_probe(torch, cases, gpu) == 0
+    line = [ln for ln in capsys.readouterr().out.splitlines() if ln.startswith('{"stream_probe"')]
+    res = json.loads(line[-1])["results"]
+    for key in ("head_strided_nt", "head_strided_plain", "whole_slot_nt", "linear_nt",
+                "timed_head_strided", "dynamic_512", "dynamic_1024"):
+        assert 1.0 < res[key]["tbps"] < 8.0, (key, res[key])
+    for key in ("timed_head_strided", "dynamic_512", "dynamic_1024"):
+        e = res[key]["wg_end_us"]
+        assert 0 < e["min"] <= e["p10"] <= e["p50"] <= e["p90"] <= e["max"], (key, e)
+        assert e["max"] < 2 * res[key]["median_us"], (key, e, res[key]["median_us"])
