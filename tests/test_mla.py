@@ -293,6 +293,25 @@ def test_balanced_flashmla_grid(gpu, s_q, h_q, causal):
         check(run_balanced(case, causal, nwg), want, f"bal s_q{s_q}/h{h_q}/c{causal}/n{nwg}")
 
 
+@pytest.mark.parametrize("s_q", [3, 4, 8])
+@pytest.mark.parametrize("h_q", [16, 128])
+def test_more_query_tokens(gpu, s_q, h_q):
+    # Beyond FlashMLA's benchmark grid: 3, 4 and 8 query tokens per request
+    # (speculative decoding), causal and not, through both launches. With
+    # h_q = 128 the rows span 3 to 8 row groups of 128; with causal masking
+    # each query token's key limit differs by one, and the short requests
+    # (down to s_q tokens) leave the first query tokens a single key.
+    S_list = mla_seq_lens(5, 600, seed=s_q * h_q, s_q=s_q) + [s_q, s_q + 31]
+    print(f"mla s_q={s_q} h_q={h_q} S={S_list}", flush=True)
+    case = mla_case(S_list, s_q, h_q, seed=s_q + h_q)
+    for causal in (False, True):
+        want = oracle(case, causal)
+        for ns in (1, 3):
+            check(run(case, causal, ns), want, f"s_q{s_q}/h{h_q}/c{causal}/ns{ns}")
+        for nwg in (7, 256):
+            check(run_balanced(case, causal, nwg), want, f"bal s_q{s_q}/h{h_q}/c{causal}/n{nwg}")
+
+
 @pytest.mark.parametrize("S_list", [[0], [0, 0, 5], [1, 0, 64, 65, 0, 33], [3000], [31, 32, 33],
                                     [0, 2000, 0, 1, 700]])
 def test_balanced_ragged_and_empty(gpu, S_list):
