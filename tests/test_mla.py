@@ -312,6 +312,31 @@ def test_more_query_tokens(gpu, s_q, h_q):
             check(run_balanced(case, causal, nwg), want, f"bal s_q{s_q}/h{h_q}/c{causal}/n{nwg}")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes(gpu, seed):
+    # Seeded random combinations the fixed grids above do not pair up: batch
+    # 1-9, 1-4 query tokens, any head count 1-140, block sizes from 1 to 128
+    # (multiples of 32 and not), lengths from 0 to 2500 (some shorter than
+    # s_q, so that causal rows can have no key), causal or not; each through
+    # fixed splits (1-6) and the balanced launch (1-300 shares).
+    rng = np.random.RandomState(1000 + seed)
+    B = int(rng.randint(1, 10))
+    s_q = int(rng.randint(1, 5))
+    h_q = int(rng.randint(1, 141))
+    bs = int(rng.choice([1, 7, 16, 32, 48, 64, 96, 128]))
+    S_list = [int(x) for x in rng.randint(0, 2501, size=B)]
+    S_list[int(rng.randint(0, B))] = int(rng.randint(0, s_q + 1))
+    causal = bool(rng.randint(0, 2))
+    ns = int(rng.randint(1, 7))
+    nwg = int(rng.randint(1, 301))
+    print(f"mla random seed={seed}: B={B} s_q={s_q} h_q={h_q} bs={bs} causal={causal} "
+          f"ns={ns} nwg={nwg} S={S_list}", flush=True)
+    case = mla_case(S_list, s_q, h_q, bs=bs, seed=seed)
+    want = oracle(case, causal)
+    check(run(case, causal, ns), want, f"random{seed}/ns{ns}")
+    check(run_balanced(case, causal, nwg), want, f"random{seed}/bal{nwg}")
+
+
 @pytest.mark.parametrize("S_list", [[0], [0, 0, 5], [1, 0, 64, 65, 0, 33], [3000], [31, 32, 33],
                                     [0, 2000, 0, 1, 700]])
 def test_balanced_ragged_and_empty(gpu, S_list):
