@@ -24,7 +24,7 @@ import pytest
 import torch
 
 import capi
-from binding import gqa_decode_balanced, gqa_decode_v2, prefer_balanced
+from binding import gqa_decode_balanced, gqa_decode_v1, gqa_decode_v2, prefer_balanced
 from cases import config_seq_lens, make_case, make_config_case
 from gpu_util import assert_close, numpy_oracle, oracle
 from test_gqa_decode import CASES, ref_case
@@ -170,3 +170,34 @@ def test_balanced_ops(gpu):
     with pytest.raises(RuntimeError, match="at most 16"):
         gqa_decode_balanced(torch.zeros(1, 136, 128, dtype=torch.bfloat16, device=q.device), k, v,
                             bt[:1], sl[:1], SCALE)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_shapes(gpu, seed):
+    # Seeded random combinations the fixed grids do not pair up: 1-6
+    # requests of 1-3000 tokens, 1-16 kv-heads of 1-16 q-heads each, block
+    # sizes 1-128 (multiples of 16 and not), NaN in every slot no request
+    # owns; through v1, v2 at its automatic choice and at 1-40 splits, and the
+    # balanced launch with 1-400 workgroups where it serves the shape (groups
+    # of up to 4, or up to 16 with 4 or 8 kv-heads; elsewhere its workspace
+    # size is 0), all against the oracle.
+    rng = np.random.default_rng(2000 + seed)
+    B = int(rng.integers(1, 7))
+    Hkv = int(rng.choice([1, 2, 4, 8, 16]))
+    G = int(rng.integers(1, 17))
+    bs = int(rng.choice([1, 7, 16, 24, 32, 64, 128]))
+    S_list = [int(x) for x in rng.integers(1, 3001, size=B)]
+    ns = int(rng.integers(1, 41))
+    nwg = int(rng.integers(1, 401))
+    print(f"random seed={seed}: B={B} Hq={G * Hkv} Hkv={Hkv} bs={bs} ns={ns} nwg={nwg} "
+          f"S={S_list}", flush=True)
+    case = ref_case(dict(S_list=S_list, Hq=G * Hkv, Hkv=Hkv, bs=bs), seed=seed)
+    want = numpy_oracle(case, SCALE)
+    label = f"random{seed}"
+    assert_close(gqa_decode_v1(*case, SCALE), want, ATOL, RTOL, f"{label}/v1")
+    assert_close(gqa_decode_v2(*case, SCALE, num_splits=0), want, ATOL, RTOL, f"{label}/auto")
+    assert_close(gqa_decode_v2(*case, SCALE, num_splits=ns), want, ATOL, RTOL, f"{label}/ns{ns}")
+    if G <= 4 or Hkv in (4, 8):
+        assert_close(balanced(case, nwg=nwg), want, ATOL, RTOL, f"{label}/bal{nwg}")
+    else:
+        assert capi.balanced_workspace_bytes(B, G * Hkv, Hkv, nwg) == 0
