@@ -1,6 +1,6 @@
 """ctypes view of the C ABI in include/gqa_decode.h (libgqa_decode_hip.so).
 
-This is the binding a non-torch host would write; the
+This is the binding a non-torch host would write over the same library; the
 tests use it to drive the launchers directly -- caller-owned workspace,
 error codes -- and to check that every declared entry point is exported.
 Pointer arguments take integers (e.g. ``tensor.data_ptr()``); the stream is a
