@@ -51,9 +51,10 @@ def main(argv=None):
     import capi
     import cases
 
-    capi.LIB_PATH = os.path.abspath(args.lib)
-    capi.lib()
-    raw = ctypes.CDLL(capi.LIB_PATH)
+    # Its own handle on the profiling build: the launches below must run the
+    # build whose table is read back, whatever library this process loaded
+    # before (capi.lib(), the torch extension).
+    raw = capi.bind(os.path.abspath(args.lib))
     if not hasattr(raw, "mla_decode_phase_table"):
         sys.exit(f"{args.lib} is not a MLA_PHASE_TIMING build")
     raw.mla_decode_phase_table.argtypes = [ctypes.c_void_p, ctypes.c_int]
@@ -65,14 +66,14 @@ def main(argv=None):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, h_q, s_q, dtype=torch.float32, device=dev)
-    wsb = capi.mla_balanced_workspace_bytes(B, s_q, h_q, cus)
+    wsb = raw.mla_decode_balanced_workspace_bytes(B, s_q, h_q, cus)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
     largs = (q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(), out.data_ptr(),
              lse.data_ptr(), B, s_q, h_q, bs, bt.shape[1], 576 ** -0.5, 0, cus, ws.data_ptr(), wsb,
              torch.cuda.current_stream().cuda_stream)
 
     def step():
-        if capi.mla_balanced_launch(*largs) != 0:
+        if raw.mla_decode_balanced_launch(*largs) != 0:
             raise RuntimeError("mla_decode_balanced_launch failed")
 
     for _ in range(20):

@@ -41,59 +41,66 @@ def declared_mla_functions():
 
 
 def lib():
+    """The in-tree library (LIB_PATH), loaded and bound once per process."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise OSError(f"{LIB_PATH} missing: run `python mla-decode-kernels_amd/build.py`")
-        L = ctypes.CDLL(LIB_PATH)
-        for name in ("gqa_decode_v0_launch", "gqa_decode_v1_launch"):
-            fn = getattr(L, name)
-            fn.argtypes = _LAUNCH_ARGS + [_vp]
-            fn.restype = _i
-        L.gqa_decode_v2_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, _vp, _vp, _vp]
-        L.gqa_decode_v2_launch.restype = _i
-        L.gqa_decode_v2_partial_launch.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
-                                                   ctypes.c_float, _i, _vp, _vp, _vp, _vp]
-        L.gqa_decode_v2_partial_launch.restype = _i
-        L.gqa_decode_v2_merge_launch.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
-        L.gqa_decode_v2_merge_launch.restype = _i
-        L.gqa_decode_v2_workspace_bytes.argtypes = [_i, _i, _i]
-        L.gqa_decode_v2_workspace_bytes.restype = ctypes.c_size_t
-        L.gqa_decode_v2_fused_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
-        L.gqa_decode_v2_fused_launch.restype = _i
-        L.gqa_decode_v2_fused_workspace_bytes.argtypes = [_i, _i, _i]
-        L.gqa_decode_v2_fused_workspace_bytes.restype = ctypes.c_size_t
-        L.gqa_decode_v2_fused_reset.argtypes = [_vp, ctypes.c_size_t, _i, _i, _i, _vp]
-        L.gqa_decode_v2_fused_reset.restype = _i
-        L.gqa_decode_pick_num_splits.argtypes = [_i, _i, _i, _i, _i, _i]
-        L.gqa_decode_pick_num_splits.restype = _i
-        L.gqa_decode_balanced_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
-        L.gqa_decode_balanced_launch.restype = _i
-        L.gqa_decode_balanced_workspace_bytes.argtypes = [_i, _i, _i, _i]
-        L.gqa_decode_balanced_workspace_bytes.restype = ctypes.c_size_t
-        for name in ("gqa_decode_balanced_partial_launch", "gqa_decode_balanced_merge_launch"):
-            fn = getattr(L, name)
-            fn.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
-            fn.restype = _i
-        L.gqa_decode_balanced_launch_noalloc.argtypes = _LAUNCH_ARGS + [_i, _vp]
-        L.gqa_decode_balanced_launch_noalloc.restype = _i
-        L.gqa_decode_prefer_balanced.argtypes = [_i, _i, _i, _i, _i, _i]
-        L.gqa_decode_prefer_balanced.restype = _i
-        for fn in (L.mla_decode_launch, L.mla_decode_splitkv_launch, L.mla_decode_balanced_launch):
-            fn.argtypes = [_vp] * 6 + [_i] * 5 + [ctypes.c_float, _i, _i, _vp, ctypes.c_size_t,
-                                                  _vp]
-            fn.restype = _i
-        L.mla_decode_combine_launch.argtypes = [_vp, ctypes.c_size_t, _vp, _vp, _i, _i, _i, _i,
-                                                _vp]
-        L.mla_decode_combine_launch.restype = _i
-        L.mla_decode_balanced_workspace_bytes.argtypes = [_i] * 4
-        L.mla_decode_balanced_workspace_bytes.restype = ctypes.c_size_t
-        L.mla_decode_workspace_bytes.argtypes = [_i] * 4
-        L.mla_decode_workspace_bytes.restype = ctypes.c_size_t
-        L.mla_decode_pick_num_splits.argtypes = [_i] * 6
-        L.mla_decode_pick_num_splits.restype = _i
-        _lib = L
+        _lib = bind(LIB_PATH)
     return _lib
+
+
+def bind(path):
+    """A build of the library at `path` with every entry point's signature set
+    (a separate handle from lib(): tools load profiling builds this way)."""
+    if not os.path.exists(path):
+        raise OSError(f"{path} missing: run `python mla-decode-kernels_amd/build.py`")
+    L = ctypes.CDLL(path)
+    for name in ("gqa_decode_v0_launch", "gqa_decode_v1_launch"):
+        fn = getattr(L, name)
+        fn.argtypes = _LAUNCH_ARGS + [_vp]
+        fn.restype = _i
+    L.gqa_decode_v2_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, _vp, _vp, _vp]
+    L.gqa_decode_v2_launch.restype = _i
+    L.gqa_decode_v2_partial_launch.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                               ctypes.c_float, _i, _vp, _vp, _vp, _vp]
+    L.gqa_decode_v2_partial_launch.restype = _i
+    L.gqa_decode_v2_merge_launch.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    L.gqa_decode_v2_merge_launch.restype = _i
+    L.gqa_decode_v2_workspace_bytes.argtypes = [_i, _i, _i]
+    L.gqa_decode_v2_workspace_bytes.restype = ctypes.c_size_t
+    L.gqa_decode_v2_fused_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
+    L.gqa_decode_v2_fused_launch.restype = _i
+    L.gqa_decode_v2_fused_workspace_bytes.argtypes = [_i, _i, _i]
+    L.gqa_decode_v2_fused_workspace_bytes.restype = ctypes.c_size_t
+    L.gqa_decode_v2_fused_reset.argtypes = [_vp, ctypes.c_size_t, _i, _i, _i, _vp]
+    L.gqa_decode_v2_fused_reset.restype = _i
+    L.gqa_decode_pick_num_splits.argtypes = [_i, _i, _i, _i, _i, _i]
+    L.gqa_decode_pick_num_splits.restype = _i
+    L.gqa_decode_balanced_launch.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
+    L.gqa_decode_balanced_launch.restype = _i
+    L.gqa_decode_balanced_workspace_bytes.argtypes = [_i, _i, _i, _i]
+    L.gqa_decode_balanced_workspace_bytes.restype = ctypes.c_size_t
+    for name in ("gqa_decode_balanced_partial_launch", "gqa_decode_balanced_merge_launch"):
+        fn = getattr(L, name)
+        fn.argtypes = _LAUNCH_ARGS + [_i, _vp, ctypes.c_size_t, _vp]
+        fn.restype = _i
+    L.gqa_decode_balanced_launch_noalloc.argtypes = _LAUNCH_ARGS + [_i, _vp]
+    L.gqa_decode_balanced_launch_noalloc.restype = _i
+    L.gqa_decode_prefer_balanced.argtypes = [_i, _i, _i, _i, _i, _i]
+    L.gqa_decode_prefer_balanced.restype = _i
+    for fn in (L.mla_decode_launch, L.mla_decode_splitkv_launch, L.mla_decode_balanced_launch):
+        fn.argtypes = [_vp] * 6 + [_i] * 5 + [ctypes.c_float, _i, _i, _vp, ctypes.c_size_t,
+                                              _vp]
+        fn.restype = _i
+    L.mla_decode_combine_launch.argtypes = [_vp, ctypes.c_size_t, _vp, _vp, _i, _i, _i, _i,
+                                            _vp]
+    L.mla_decode_combine_launch.restype = _i
+    L.mla_decode_balanced_workspace_bytes.argtypes = [_i] * 4
+    L.mla_decode_balanced_workspace_bytes.restype = ctypes.c_size_t
+    L.mla_decode_workspace_bytes.argtypes = [_i] * 4
+    L.mla_decode_workspace_bytes.restype = ctypes.c_size_t
+    L.mla_decode_pick_num_splits.argtypes = [_i] * 6
+    L.mla_decode_pick_num_splits.restype = _i
+    return L
 
 
 def v0_launch(*args):

@@ -4,6 +4,7 @@ reduction of synthetic rocprofv3 CSV output)."""
 import csv
 import json
 import os
+import re
 
 import pytest
 
@@ -141,10 +142,32 @@ def test_mla_phase_table(gpu, capsys):
         pytest.skip("profiling build not present (build.py --variant phase --define MLA_PHASE_TIMING=1)")
     import mla_phases
 
+    # The process has already loaded the in-tree library (capi.lib(), the
+    # torch extension): the tool must still run the profiling build.
+    import capi
+
+    capi.lib()
     assert mla_phases.main(["--config", "mla_4k", "--steps", "3"]) == 0
     out = capsys.readouterr().out
     assert "Cycles per full interval and wave" in out
-    assert "| PV-first 0-3 |" in out and "| QK-first 4-7 |" in out
+    m = re.search(r"Split kernel per wave: (\d+) cycles at (\d+) MHz", out)
+    assert m, out
+    cycles, mhz = int(m.group(1)), int(m.group(2))
+    assert cycles > 10000 and 500 < mhz < 3000, (cycles, mhz)
+    rows = {}
+    for ln in out.splitlines():
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        if cells[0] in ("PV-first 0-3", "QK-first 4-7"):
+            rows[cells[0]] = [int(c) for c in cells[1:]]
+    for name, vals in rows.items():
+        # copies .. barrier add up to the total; an interval of 32 tokens x 128
+        # rows holds 2176 MFMA cycles per SIMD, so it cannot be shorter.
+        assert sum(vals[:-1]) == pytest.approx(vals[-1], abs=6), (name, vals)
+        assert 2176 < vals[-1] < 20000, (name, vals)
+    assert len(rows) == 2
+    # The full intervals are most of a wave's time at mla_4k.
+    share = re.search(r"\| (\d+) \((\d+)%\) \|", out)
+    assert share and 50 <= int(share.group(2)) <= 100, out
 
 
 @pytest.mark.gpu
