@@ -201,3 +201,59 @@ def test_random_shapes(gpu, seed):
         assert_close(balanced(case, nwg=nwg), want, ATOL, RTOL, f"{label}/bal{nwg}")
     else:
         assert capi.balanced_workspace_bytes(B, G * Hkv, Hkv, nwg) == 0
+
+
+@pytest.mark.parametrize("kind", ["v2_ns1", "v2_ns8", "balanced", "balanced_noalloc"])
+def test_graph_replay(gpu, kind):
+    # The C-ABI launches captured once in a HIP graph and replayed, as a
+    # serving loop runs them: each replay (on new queries written between
+    # replays, with the eager launch itself in between) equals the eager
+    # launch on the same inputs bit for bit. None of these launches records a
+    # memset or allocates.
+    case = ref_case(dict(S_list=[700, 64, 3000, 1, 2000], Hq=32, Hkv=8, bs=16), seed=21)
+    q, k, v, bt, sl = case
+    B, Hq = q.shape[:2]
+    Hkv, bs, mb = k.shape[2], k.shape[1], bt.shape[1]
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr())
+
+    def make_launch(out):
+        if kind.startswith("v2"):
+            ns = int(kind[len("v2_ns"):])
+            acc = torch.empty(B * Hq * ns * 128, dtype=torch.float32, device=q.device)
+            m = torch.empty(B * Hq * ns, dtype=torch.float32, device=q.device)
+            l = torch.empty(B * Hq * ns, dtype=torch.float32, device=q.device)
+            return lambda: capi.v2_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, SCALE, ns,
+                                          acc.data_ptr(), m.data_ptr(), l.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream)
+        if kind == "balanced":
+            nbytes = capi.balanced_workspace_bytes(B, Hq, Hkv, 0)
+            ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+            return lambda: capi.balanced_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, SCALE, 0,
+                                                ws.data_ptr(), nbytes,
+                                                torch.cuda.current_stream().cuda_stream)
+        return lambda: capi.balanced_launch_noalloc(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb,
+                                                    SCALE, 0,
+                                                    torch.cuda.current_stream().cuda_stream)
+
+    out = torch.empty_like(q)
+    launch = make_launch(out)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert launch() == 0  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert launch() == 0
+    eager_out = torch.empty_like(q)
+    eager = make_launch(eager_out)
+    gen = torch.Generator(device="cpu").manual_seed(22)
+    for rep in range(4):
+        q.copy_((0.5 * torch.randn(q.shape, generator=gen)).to(q.device, torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert eager() == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out), f"{kind}: replay {rep} differs from the eager launch"
+    assert_close(out, numpy_oracle(case, SCALE), ATOL, RTOL, f"{kind}/graph")
