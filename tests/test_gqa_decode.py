@@ -204,6 +204,51 @@ def test_merge_entry_point(gpu):
     assert_close(out, want, 1e-2, 1e-2, "merge")
 
 
+@pytest.mark.parametrize("ranks", [2, 3])
+def test_context_parallel_shards(gpu, ranks):
+    """Sharding by tokens (context parallelism) on one GPU: each "rank" holds a
+    contiguous range of every request's blocks -- its own block table and
+    lengths, possibly empty -- and computes one state per (request, q-head)
+    with the exported partial launch; the states, placed in rank order as an
+    all-gather delivers them, go through the exported merge launch. The result
+    matches the oracle on the whole sequences."""
+    S_list, Hq, Hkv, bs = [3000, 517, 1, 2048, 40], 32, 8, 16
+    case = ref_case(dict(S_list=S_list, Hq=Hq, Hkv=Hkv, bs=bs), seed=31)
+    q, k, v, bt, sl = case
+    B = q.shape[0]
+    bt_h = bt.cpu()
+    accs, ms, ls = [], [], []
+    for r in range(ranks):
+        lens, rows = [], []
+        for b, S in enumerate(S_list):
+            nb = (S + bs - 1) // bs
+            lo, hi = r * nb // ranks, (r + 1) * nb // ranks
+            lens.append(max(0, min(S, hi * bs) - lo * bs))
+            rows.append(bt_h[b, lo:hi])
+        mb = max(1, max(len(x) for x in rows))
+        bt_r = torch.full((B, mb), -1, dtype=torch.int32)
+        for b, x in enumerate(rows):
+            bt_r[b, :len(x)] = x
+        bt_r = bt_r.to(q.device)
+        sl_r = torch.tensor(lens, dtype=torch.int32, device=q.device)
+        _, acc, m, l = alloc_ws(B, Hq, 1, q.device)
+        assert capi.v2_partial_launch(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt_r.data_ptr(),
+                                      sl_r.data_ptr(), B, Hq, Hkv, bs, mb, SCALE, 1,
+                                      acc.data_ptr(), m.data_ptr(), l.data_ptr(),
+                                      stream_ptr()) == 0
+        accs.append(acc)
+        ms.append(m)
+        ls.append(l)
+    acc_all = torch.cat(accs, dim=2).contiguous()  # [B, Hq, ranks, D]
+    m_all = torch.cat(ms, dim=2).contiguous()
+    l_all = torch.cat(ls, dim=2).contiguous()
+    out = torch.empty_like(q)
+    assert capi.v2_merge_launch(acc_all.data_ptr(), m_all.data_ptr(), l_all.data_ptr(),
+                                out.data_ptr(), B, Hq, ranks, stream_ptr()) == 0
+    torch.cuda.synchronize()
+    assert_close(out, numpy_oracle(case, SCALE), ATOL, RTOL, f"cp{ranks}")
+
+
 def test_capi_v2_matches_op(gpu):
     case = ref_case(CASES["a_base"])
     q, k, v, bt, sl = case
