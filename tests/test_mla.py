@@ -190,6 +190,59 @@ def test_split_and_combine_launches(gpu, ns):
     assert torch.equal(out, want[0]) and torch.equal(lse, want[1])
 
 
+@pytest.mark.parametrize("ranks", [2, 3])
+def test_context_parallel_shards(gpu, ranks):
+    # Sharding long requests by tokens across GPUs, on one GPU: each "rank"
+    # holds a contiguous range of every request's blocks (its own block table
+    # and lengths, some empty) and runs the split launch with 2 splits; the
+    # workspace states, placed in rank order per (request, query row) as an
+    # all-gather delivers them, go through the combine launch with 2 x ranks
+    # splits. out and lse match the oracle on the whole sequences.
+    S_list, s_q, h_q, bs = [2900, 450, 1, 1300, 64], 2, 32, 64
+    case = mla_case(S_list, s_q, h_q, bs=bs, seed=41)
+    q, kv, bt, sl = case
+    B, R = len(S_list), s_q * h_q
+    bt_h = bt.cpu()
+    sp = torch.cuda.current_stream().cuda_stream
+    accs, ms, ls = [], [], []
+    for r in range(ranks):
+        lens, rows = [], []
+        for b, S in enumerate(S_list):
+            nb = (S + bs - 1) // bs
+            lo, hi = r * nb // ranks, (r + 1) * nb // ranks
+            lens.append(max(0, min(S, hi * bs) - lo * bs))
+            rows.append(bt_h[b, lo:hi])
+        mb = max(1, max(len(x) for x in rows))
+        bt_r = torch.full((B, mb), -1, dtype=torch.int32)
+        for b, x in enumerate(rows):
+            bt_r[b, :len(x)] = x
+        bt_r = bt_r.to(q.device)
+        sl_r = torch.tensor(lens, dtype=torch.int32, device=q.device)
+        wsb = capi.mla_workspace_bytes(B, s_q, h_q, 2)
+        ws = torch.empty(wsb // 4, dtype=torch.float32, device=q.device)
+        scratch_out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=q.device)
+        scratch_lse = torch.empty(B, h_q, s_q, dtype=torch.float32, device=q.device)
+        assert capi.mla_splitkv_launch(q.data_ptr(), kv.data_ptr(), bt_r.data_ptr(),
+                                       sl_r.data_ptr(), scratch_out.data_ptr(),
+                                       scratch_lse.data_ptr(), B, s_q, h_q, bs, mb, SCALE, 0, 2,
+                                       ws.data_ptr(), wsb, sp) == 0
+        states = B * R * 2
+        accs.append(ws[:states * 512].view(B * R, 2, 512))
+        ms.append(ws[states * 512:states * 513].view(B * R, 2))
+        ls.append(ws[states * 513:states * 514].view(B * R, 2))
+    ns = 2 * ranks
+    gathered = torch.cat([torch.cat(accs, dim=1).flatten(), torch.cat(ms, dim=1).flatten(),
+                          torch.cat(ls, dim=1).flatten()])
+    wsb = capi.mla_workspace_bytes(B, s_q, h_q, ns)
+    assert gathered.numel() * 4 == wsb
+    out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, h_q, s_q, dtype=torch.float32, device=q.device)
+    assert capi.mla_combine_launch(gathered.data_ptr(), wsb, out.data_ptr(), lse.data_ptr(), B,
+                                   s_q, h_q, ns, sp) == 0
+    torch.cuda.synchronize()
+    check((out, lse), oracle(case, False), f"cp{ranks}")
+
+
 @pytest.mark.parametrize("ns", [1, 3])
 def test_late_dominant_key(gpu, ns):
     # A key far above everything before it (score ~ 2|q|^2, ~70 in log2
