@@ -37,15 +37,15 @@ def host(t):
         if t.dtype == torch.bfloat16 else t.cpu().numpy()
 
 
-def oracle(case, causal, batches=None):
+def oracle(case, causal, batches=None, scale=SCALE):
     q, kv, bt, sl = case
     qh, bth, slh = host(q), host(bt), host(sl)
     if batches is not None:
         qh, bth, slh = qh[batches], bth[batches], slh[batches]
-    return c_oracle.mla_decode_ref(qh, host(kv), bth, slh, SCALE, causal=causal)
+    return c_oracle.mla_decode_ref(qh, host(kv), bth, slh, scale, causal=causal)
 
 
-def run(case, causal, ns):
+def run(case, causal, ns, scale=SCALE):
     q, kv, bt, sl = case
     B, s_q, h_q, _ = q.shape
     out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=q.device)
@@ -53,7 +53,7 @@ def run(case, causal, ns):
     wsb = capi.mla_workspace_bytes(B, s_q, h_q, ns)
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
     rc = capi.mla_launch(q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(), out.data_ptr(),
-                         lse.data_ptr(), B, s_q, h_q, kv.shape[1], bt.shape[1], SCALE,
+                         lse.data_ptr(), B, s_q, h_q, kv.shape[1], bt.shape[1], scale,
                          int(causal), ns, ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
@@ -318,7 +318,7 @@ def test_overflowing_late_key(gpu, ns):
 # --------------------------------------------------------- token-balanced launch
 
 
-def run_balanced(case, causal, nwg):
+def run_balanced(case, causal, nwg, scale=SCALE):
     q, kv, bt, sl = case
     B, s_q, h_q, _ = q.shape
     out = torch.empty(B, s_q, h_q, 512, dtype=torch.bfloat16, device=q.device)
@@ -327,7 +327,7 @@ def run_balanced(case, causal, nwg):
     ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=q.device)
     rc = capi.mla_balanced_launch(q.data_ptr(), kv.data_ptr(), bt.data_ptr(), sl.data_ptr(),
                                   out.data_ptr(), lse.data_ptr(), B, s_q, h_q, kv.shape[1],
-                                  bt.shape[1], SCALE, int(causal), nwg, ws.data_ptr(), wsb,
+                                  bt.shape[1], scale, int(causal), nwg, ws.data_ptr(), wsb,
                                   torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     torch.cuda.synchronize()
@@ -388,6 +388,20 @@ def test_random_shapes(gpu, seed):
     want = oracle(case, causal)
     check(run(case, causal, ns), want, f"random{seed}/ns{ns}")
     check(run_balanced(case, causal, nwg), want, f"random{seed}/bal{nwg}")
+
+
+@pytest.mark.parametrize("scale", [0.01, 0.2, 1.0])
+def test_softmax_scales(gpu, scale):
+    # softmax_scale other than 1/sqrt(576): small (nearly uniform weights over
+    # every key) and large (scores spread over hundreds of log2 units, nearly
+    # one-hot rows; rows whose later tiles beat their first tile's maximum by
+    # more than the reference slack take the second pass).
+    case = mla_case(mla_seq_lens(4, 800, seed=51, s_q=2), 2, 32, seed=51)
+    for causal in (False, True):
+        want = oracle(case, causal, scale=scale)
+        check(run(case, causal, 3, scale=scale), want, f"scale{scale}/c{causal}/ns3")
+        check(run_balanced(case, causal, 37, scale=scale), want,
+              f"scale{scale}/c{causal}/bal37")
 
 
 @pytest.mark.parametrize("S_list", [[0], [0, 0, 5], [1, 0, 64, 65, 0, 33], [3000], [31, 32, 33],
