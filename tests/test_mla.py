@@ -390,6 +390,21 @@ def test_random_shapes(gpu, seed):
     check(run_balanced(case, causal, nwg), want, f"random{seed}/bal{nwg}")
 
 
+def test_long_request(gpu):
+    # One request of 65536 tokens with a short one beside it: the balanced
+    # launch cuts it into ~256 pieces of ~8 tiles and the merge folds a few
+    # hundred states per row; fixed splits take it at 64 and 128 (the most
+    # accepted) splits.
+    S_list = [65536, 300]
+    print(f"mla long request S={S_list}", flush=True)
+    case = mla_case(S_list, 1, 128, seed=61)
+    for causal in (False, True):
+        want = oracle(case, causal)
+        check(run_balanced(case, causal, 256), want, f"long/c{causal}/bal256")
+        for ns in (64, 128):
+            check(run(case, causal, ns), want, f"long/c{causal}/ns{ns}")
+
+
 @pytest.mark.parametrize("scale", [0.01, 0.2, 1.0])
 def test_softmax_scales(gpu, scale):
     # softmax_scale other than 1/sqrt(576): small (nearly uniform weights over
