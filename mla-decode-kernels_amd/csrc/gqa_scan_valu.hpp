@@ -85,6 +85,10 @@ template <int GH, int P, int DEPTH, bool kBlockUniform, bool kPinIssue = false>
 __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, int hkv,
                                              const uint4 (&qf)[GH], int seg_start, int seg_end,
                                              int ph, int r, int c, WaveState<GH>& st) {
+  // The steady-state loop leaves each wave's last tile (the only one that can
+  // reach past seg_end) to the masked tail only with two or more tiles in
+  // flight.
+  static_assert(DEPTH >= 2, "scan_segment needs at least two tiles in flight");
   const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
   const int my_tiles = ntiles > ph ? (ntiles - ph + P - 1) / P : 0;
   const uint32_t row_elems = (uint32_t)a.Hkv * kHeadDim;  // elements between slots
