@@ -46,6 +46,7 @@ sys.path.insert(0, os.path.join(PKG_DIR, "bench"))
 
 METRIC = ("median µs and % of HBM KV-bytes SoL, 32Q/8KV d=128 S=8192 B=32 block=16")
 TRAFFIC_FILE = os.path.join(REPO_ROOT, "profiles", "traffic.txt")
+SWEEP_SPLITS = [1, 2, 4, 8, 16, 32, 64]  # --sweep: BASELINE.json's c2 and c3 sweeps
 MLA_NAMES = [f"mla_{k}k{sfx}" for sfx in ("", "_sq2") for k in (4, 8, 16, 32)]
 MLA_METRIC = ("median µs, TFLOP/s and GB/s of MLA absorbed decode (FlashMLA's accounting), "
               "b=128 h_q=128 h_kv=1 d=576 dv=512 block=64 varlen")
@@ -68,7 +69,8 @@ def parse_args(argv=None):
     ap.add_argument("--kernel", default="v2", choices=["v0", "v1", "v2", "balanced"],
                     help="v2 with --num-splits 0 makes the op's automatic choice (balanced or split)")
     ap.add_argument("--num-splits", type=int, default=0, help="v2 split count (0 = heuristic)")
-    ap.add_argument("--sweep", action="store_true", help="also time v2 over a num_splits sweep")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also time v2 at each of SWEEP_SPLITS splits, as the step is timed")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="oracle threads (default: OMP_NUM_THREADS, else the CPUs this process "
@@ -116,6 +118,42 @@ def kernel_name(kernel, group, balanced=False, hkv=8):
         return ("gqa_decode_balanced_mfma_kernel" if hkv in (4, 8)
                 else "gqa_decode_balanced_kernel")
     return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
+
+
+def ramp(torch, step, seconds, warmup):
+    """Clock ramp: the GPU takes a few hundred milliseconds of load to reach
+    its steady clocks, far longer than a few short steps; run untimed steps
+    for `seconds`, then `warmup` more."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+
+def timed_steps(torch, step, stream, K):
+    """Time exactly K calls of step() back to back on `stream`. Events sit only
+    between groups of steps (an event between two kernels delays the second
+    one), so each group's average is the steady-state step time. Returns the
+    median group average (us), the sorted group averages and the wall time (s)."""
+    groups = max(1, min(10, K // 5))
+    bounds = [round(g * K / groups) for g in range(groups + 1)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for g in range(groups):
+        ev[g].record(stream)
+        for _ in range(bounds[g + 1] - bounds[g]):
+            step()
+    ev[groups].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    group_us = sorted(ev[g].elapsed_time(ev[g + 1]) * 1e3 / (bounds[g + 1] - bounds[g])
+                      for g in range(groups))
+    return group_us[groups // 2], group_us, wall
 
 
 def main(argv=None):
@@ -217,37 +255,11 @@ def main(argv=None):
             if rc != 0:
                 raise RuntimeError(f"launch failed: hipError_t {rc}")
 
-    # Clock ramp: the GPU takes a few hundred milliseconds of load to reach its
-    # steady clocks, far longer than W short steps; run untimed steps for
-    # --ramp-seconds first, then the W warmup steps.
-    t_ramp = time.perf_counter() + args.ramp_seconds
-    while time.perf_counter() < t_ramp:
-        for _ in range(8):
-            step()
-        torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    ramp(torch, step, args.ramp_seconds, args.warmup)
 
-    # Timed region: exactly K steps back to back. Events sit only between
-    # groups of steps (an event between two kernels delays the second one), so
-    # each group's average is the steady-state step time; value = their median.
+    # Timed region: exactly K steps back to back.
+    median_us, group_us, wall = timed_steps(torch, step, stream, args.steps)
     K = args.steps
-    groups = max(1, min(10, K // 5))
-    bounds = [round(g * K / groups) for g in range(groups + 1)]
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for g in range(groups):
-        ev[g].record(stream)
-        for _ in range(bounds[g + 1] - bounds[g]):
-            step()
-    ev[groups].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    group_us = sorted(ev[g].elapsed_time(ev[g + 1]) * 1e3 / (bounds[g + 1] - bounds[g])
-                      for g in range(groups))
-    median_us = group_us[groups // 2]
 
     # The dominant kernel alone, K launches back to back on the same stream:
     # its average launch duration for the roofline.
@@ -279,12 +291,34 @@ def main(argv=None):
         assert torch.equal(out_op, out), "torch op and C ABI outputs differ"
 
     sweep = None
-    if args.sweep and args.kernel == "v2" and not args.lib:
+    if args.sweep and args.kernel == "v2":
+        # v2 at each split count, timed as the step above: partial + merge
+        # launches through the C ABI (one launch for one split) with a
+        # caller-owned workspace, K steps back to back after a warmup.
         sweep = {}
-        for s in [1, 2, 4, 8, 16, 32, 64, 128]:
-            ms = cases.time_op(lambda: gqa_decode_v2(*case, scale, num_splits=s), 3, 20)
-            sweep[s] = round(ms * 1e3, 2)
-            log(f"  sweep num_splits={s}: {ms * 1e3:.2f} us ({sol / (ms * 1e3) * 100:.1f}% SoL)")
+        top = max(SWEEP_SPLITS)
+        ws_s = torch.empty(B * Hq * top * (cases.D + 2), dtype=torch.float32, device=dev)
+        for s in SWEEP_SPLITS:
+            st = B * Hq * s
+            acc_s, m_s, l_s = (ws_s.data_ptr(), ws_s.data_ptr() + st * cases.D * 4,
+                               ws_s.data_ptr() + st * (cases.D + 1) * 4)
+
+            def sweep_step(s=s, acc_s=acc_s, m_s=m_s, l_s=l_s):
+                if capi.v2_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, s, acc_s,
+                                  m_s, l_s, sp) != 0:
+                    raise RuntimeError(f"v2 launch failed at num_splits={s}")
+
+            def sweep_partial(s=s, acc_s=acc_s, m_s=m_s, l_s=l_s):
+                if capi.v2_partial_launch(*ptrs, B, Hq, Hkv, bs, mb, scale, s, acc_s, m_s, l_s,
+                                          sp) != 0:
+                    raise RuntimeError(f"v2 partial launch failed at num_splits={s}")
+            ramp(torch, sweep_step, args.ramp_seconds, args.warmup)
+            us = timed_steps(torch, sweep_step, stream, K)[0]
+            part_us = timed_steps(torch, sweep_partial, stream, K)[0]
+            sweep[s] = {"us": round(us, 2), "pct_of_sol": round(sol / us * 100, 2),
+                        "partial_us": round(part_us, 2)}
+            log(f"  sweep num_splits={s}: {us:.2f} us ({sol / us * 100:.1f}% SoL), "
+                f"partial kernel {part_us:.2f} us")
 
     split_label = "balanced" if balanced else ns
     traffic = read_traffic(args.config, "v2" if balanced else args.kernel, split_label)

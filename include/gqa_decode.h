@@ -77,7 +77,15 @@ GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cac
  * kernel writes `out`. Which scan runs depends on the shape, num_splits and the
  * device's CU count (the layout rule of gqa_decode_v1_launch with
  * B * num_splits in place of B), so results are bitwise reproducible for the
- * same inputs, split count and device. Workspace layout (the reference's, v2_splitkv.cu:10-12):
+ * same inputs, split count and device. For groups of up to 4 q-heads, once
+ * num_splits reaches 4 * max(1, CUs / (B * Hkv)) -- the waves the launch gives
+ * each (request, kv-head) pair -- every split is scanned by one wave, each
+ * wave walking a run of consecutive splits; with one workgroup per pair
+ * (B * Hkv >= CUs) and at most 19 splits per wave (38 for 2-head groups, 76
+ * for 1-head groups, 25 for 3-head groups) that workgroup also merges its
+ * splits, and no merge kernel runs. out is bitwise equal to
+ * gqa_decode_v2_partial_launch followed by gqa_decode_v2_merge_launch in every
+ * case, and the workspace holds the same states. Workspace layout (the reference's, v2_splitkv.cu:10-12):
  *   ws_acc [B, Hq, num_splits, 128] fp32, ws_m / ws_l [B, Hq, num_splits] fp32
  * ws_m holds the segment's max of scale*<q,k> (natural-log units), ws_l the sum
  * of exp(score - ws_m), ws_acc the exp-weighted sum of V rows.
@@ -139,7 +147,17 @@ GQA_DECODE_API size_t gqa_decode_v2_workspace_bytes(int B, int Hq, int num_split
  * every launch leaves them zero, so one workspace serves any smaller batch
  * afterwards. Launches that share a workspace must not overlap (stream order
  * suffices). No workgroup waits on another. num_splits == 1 runs the
- * single-pass kernel. No reference counterpart: the reference's v2 is a
+ * single-pass kernel; where gqa_decode_v2_launch merges inside its one
+ * workgroup per pair (see above), this launch does the same and leaves the
+ * counters untouched. Cost elsewhere: each arriving workgroup writes back its
+ * L2 lines (the release of the arrival count), about 300 ns of its XCD's L2
+ * time, so the launch pays off with a few hundred arriving workgroups (one
+ * 8192-token request at 32 splits: 16.6 us against 19.9 us for two launches)
+ * and loses past a thousand (2048 arriving workgroups, 32 requests of 8192
+ * tokens at 8 splits with 4 waves per split: 255 us against 173 us); prefer
+ * gqa_decode_v2_launch when more than about a thousand workgroups would
+ * arrive.
+ * No reference counterpart: the reference's v2 is a
  * partial and a merge launch (kernels/gqa_decode/v2_splitkv.cu:110-125) and
  * lists the fused merge as a follow-up (README.md:386-387, 410-412). */
 GQA_DECODE_API int gqa_decode_v2_fused_launch(const uint16_t* q, const uint16_t* k_cache,

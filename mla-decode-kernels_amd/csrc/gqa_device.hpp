@@ -77,13 +77,50 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-// Sum over all 64 lanes, identical in every lane.
-__device__ __forceinline__ float wave_sum(float x) {
-  x = row16_sum(x);
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+// Cross-row exchanges on gfx950's lane-swap instructions. v_permlane16_swap_b32
+// swaps the odd 16-lane rows of its first operand with the even rows of its
+// second, v_permlane32_swap_b32 the upper 32 lanes of its first operand with
+// the lower 32 lanes of its second (pinned on the GPU by issue_probe's lane
+// probe). With x as both operands, lane l holds x[l] in one result and
+// x[l ^ 16] (x[l ^ 32]) in the other, so a commutative op of the two results
+// gives op(x[l], x[l ^ 16]) -- the bits of x op __shfl_xor(x, 16) -- in two
+// VALU instructions, where the shuffle is an LDS permute and a wait on it.
+__device__ __forceinline__ void xor16_pair(float x, float& a, float& b) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  a = __uint_as_float(p[0]);
+  b = __uint_as_float(p[1]);
 }
+__device__ __forceinline__ void xor32_pair(float x, float& a, float& b) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  a = __uint_as_float(p[0]);
+  b = __uint_as_float(p[1]);
+}
+// x[l] + x[l ^ 16], x[l] + x[l ^ 32], and the maxima, in every lane l.
+__device__ __forceinline__ float xor16_sum(float x) {
+  float a, b;
+  xor16_pair(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  float a, b;
+  xor32_pair(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  float a, b;
+  xor16_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  float a, b;
+  xor32_pair(x, a, b);
+  return fmaxf(a, b);
+}
+
+// Sum over all 64 lanes, identical in every lane.
+__device__ __forceinline__ float wave_sum(float x) { return xor32_sum(xor16_sum(row16_sum(x))); }
 
 // Max over all 64 lanes, identical in every lane (max is exact, so the order
 // of the steps does not matter).
@@ -92,8 +129,7 @@ __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp_f32<0x4E>(x));
   x = fmaxf(x, dpp_f32<0x141>(x));
   x = fmaxf(x, dpp_f32<0x140>(x));
-  x = fmaxf(x, __shfl_xor(x, 16, 64));
-  return fmaxf(x, __shfl_xor(x, 32, 64));
+  return xor32_max(xor16_max(x));
 }
 
 // Hardware 2^x (v_exp_f32): 2^-inf = 0, 2^0 = 1.

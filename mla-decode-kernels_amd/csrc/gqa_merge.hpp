@@ -30,28 +30,49 @@ __device__ __forceinline__ float2 load_coherent2(const float* p) {
   return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
 }
 
+// One split's term in the log-sum-exp fold of an output element (the
+// reference's merge, v2_splitkv.cu:92-108): with M the max of the element's
+// split maxima (natural-log units), split i's factor is f = e^(m_i - M),
+// exactly 1 for a split holding the max and 0 for an empty split
+// (m_i = -inf); the first split sets L = l_i f and A = acc_i f, every later one
+// adds l_i f and acc_i f with a fused multiply-add. Every merge in this library
+// (the merge kernel, the single-launch merges, the in-workgroup merge) folds
+// each element with these two steps, in split order, so all give the same
+// bits.
+__device__ __forceinline__ float fold_factor(float mi, float M) {
+  return mi == M ? 1.f : exp2_fast((mi - M) * kLog2e);
+}
+__device__ __forceinline__ void fold_term(bool first, float x, float f, float& acc) {
+  acc = first ? x * f : fmaf(x, f, acc);
+}
+
 // One wave folds the ns states of (b, q-head) bh, stored at state index
 // bh * ns + i (the reference's [B, Hq, ns] layout), and writes out's row bh:
-// lane i owns dims {2i, 2i + 1}. The splits are folded in index order, their
-// states loaded kBatch at a time; the first batch's loads are issued together
-// with the loads of the maxima (one split per lane), so at most kBatch splits
-// take one memory round trip. The factor of the split holding the max is
-// exactly 1, so one split merges to itself bit for bit.
+// lane i owns dims {2i, 2i + 1}. The splits are folded in index order,
+// kBatch at a time: a batch's acc rows are loaded together, and its m and l
+// with one load each (lane k holds split i0 + k's, broadcast with
+// v_readlane). The first batch's loads are issued together with the loads of
+// the maxima (one split per lane), so at most kBatch splits take one memory
+// round trip. The factor of the split holding the max is exactly 1, so one
+// split merges to itself bit for bit.
+template <int kBatch>
 __device__ __forceinline__ void merge_head(const float* __restrict__ ws_acc,
                                            const float* __restrict__ ws_m,
                                            const float* __restrict__ ws_l,
                                            uint16_t* __restrict__ out, size_t bh, int ns,
                                            int lane) {
-  constexpr int kBatch = 8;
+  static_assert(kBatch <= 64, "a batch's m and l are held one per lane");
   const size_t st0 = bh * ns;
-  float mi[kBatch], li[kBatch];
+  float mb, lb;  // lane k < kBatch: m and l of split i0 + k
   float2 av[kBatch];
   auto load_batch = [&](int i0) {
+    // Past the end: a valid split, not folded.
+    const size_t sl = st0 + min(i0 + (lane & (kBatch - 1)), ns - 1);
+    mb = ws_m[sl];
+    lb = ws_l[sl];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
-      const size_t st = st0 + min(i0 + k, ns - 1);  // past the end: a valid split, not folded
-      mi[k] = ws_m[st];
-      li[k] = ws_l[st];
+      const size_t st = st0 + min(i0 + k, ns - 1);
       av[k] = reinterpret_cast<const float2*>(ws_acc + st * kHeadDim)[lane];
     }
   };
@@ -65,16 +86,13 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ ws_acc,
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       if (i0 + k >= ns) break;
-      const float f = mi[k] == M ? 1.f : exp2_fast((mi[k] - M) * kLog2e);
-      if (i0 + k == 0) {
-        L = li[k] * f;
-        A0 = av[k].x * f;
-        A1 = av[k].y * f;
-      } else {
-        L = fmaf(li[k], f, L);
-        A0 = fmaf(av[k].x, f, A0);
-        A1 = fmaf(av[k].y, f, A1);
-      }
+      const float mi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mb), k));
+      const float li = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lb), k));
+      const float f = fold_factor(mi, M);
+      const bool first = i0 + k == 0;
+      fold_term(first, li, f, L);
+      fold_term(first, av[k].x, f, A0);
+      fold_term(first, av[k].y, f, A1);
     }
   }
   const uint32_t lo = f32_to_bf16_bits(finalize(A0, L));
@@ -136,16 +154,11 @@ __device__ __forceinline__ void merge_heads4(const float* __restrict__ ws_acc,
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       if (i0 + k >= ns) break;
-      const float f = mi[k] == M ? 1.f : exp2_fast((mi[k] - M) * kLog2e);
-      if (i0 + k == 0) {
-        L = li[k] * f;
+      const float f = fold_factor(mi[k], M);
+      const bool first = i0 + k == 0;
+      fold_term(first, li[k], f, L);
 #pragma unroll
-        for (int d = 0; d < 8; ++d) A[d] = av[k][d] * f;
-      } else {
-        L = fmaf(li[k], f, L);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) A[d] = fmaf(av[k][d], f, A[d]);
-      }
+      for (int d = 0; d < 8; ++d) fold_term(first, av[k][d], f, A[d]);
     }
   }
   if (live) {

@@ -210,8 +210,7 @@ __device__ __forceinline__ void mfma_scan_segment(const ScanArgs& a, const int* 
         s[tg][e] = valid ? c[tg][e] * a.scale_log2e : kNegInf;
         mx = fmaxf(mx, s[tg][e]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float mn = fmaxf(st.m, mx);
     const float ms = mn == kNegInf ? 0.f : mn;
     const float alpha = exp2_fast(st.m - ms);
@@ -314,8 +313,7 @@ __device__ __forceinline__ void mfma_scan_segment(const ScanArgs& a, const int* 
 // 4g + e (l summed over the 4 row groups of token slots).
 __device__ __forceinline__ void mfma_finish(const MfmaState& st, int g, float (&Me)[4],
                                             float (&Le)[4]) {
-  float L = st.lsum + __shfl_xor(st.lsum, 16, 64);
-  L += __shfl_xor(L, 32, 64);
+  const float L = xor32_sum(xor16_sum(st.lsum));
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     Me[e] = __shfl(st.m, 4 * g + e, 64);

@@ -70,53 +70,47 @@ __device__ __forceinline__ void load_q(const ScanArgs& a, int b, int h0, int nh,
   }
 }
 
-// Scan tokens [seg_start, seg_end) of kv-head hkv of the request whose block
-// table row is bt: wave ph of the P takes tiles ph, ph + P, ... of the range and
-// folds them into st. DEPTH register tiles are in flight; the steady-state
-// loop issues tile k + DEPTH - 1 before consuming tile k and has no branch, so
-// the wait before each consume covers only the tile being consumed.
-// kPinIssue puts a scheduling barrier after each tile's loads: without it the
-// compiler may sink a tile's loads below the previous tile's arithmetic, so
-// that tile is consumed right after its loads are issued. Measured on MI355X:
-// pinning speeds the token-balanced kernel up ~5% (ragged B=128 batch) and is
-// neutral to 1% slower for the split-rule kernel, whose default schedule
-// already overlaps.
-template <int GH, int P, int DEPTH, bool kBlockUniform, bool kPinIssue = false>
-__device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, int hkv,
-                                             const uint4 (&qf)[GH], int seg_start, int seg_end,
-                                             int ph, int r, int c, WaveState<GH>& st) {
-  // The steady-state loop leaves each wave's last tile (the only one that can
-  // reach past seg_end) to the masked tail only with two or more tiles in
-  // flight.
-  static_assert(DEPTH >= 2, "scan_segment needs at least two tiles in flight");
-  const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
-  const int my_tiles = ntiles > ph ? (ntiles - ph + P - 1) / P : 0;
-  const uint32_t row_elems = (uint32_t)a.Hkv * kHeadDim;  // elements between slots
-  const uint16_t* kbase = a.k_cache + (size_t)hkv * kHeadDim + 8 * c;
-  const uint16_t* vbase = a.v_cache + (size_t)hkv * kHeadDim + 8 * c;
-  const int bs = a.block_size;
+// The tile work of one wave on kv-head hkv of the request whose block table
+// row is bt: issue() loads the K and V rows of the 16-token tile starting at
+// token ts, consume() folds a loaded tile into the wave's state. Tokens at or
+// past `end` (the end of the segment being scanned) are never read: their
+// loads read the tile's first token instead (always valid), so no load touches
+// an unallocated block or a tail slot, and consume<true> masks their scores.
+template <int GH, bool kBlockUniform>
+struct ValuTiles {
+  const ScanArgs& a;
+  const int* bt;
   // The block table is read-only for the whole launch: reading it through the
   // constant address space lets the uniform block-id loads stay scalar even
   // in kernels that store to global memory between segments.
-  const __attribute__((address_space(4))) int* btc =
-      (const __attribute__((address_space(4))) int*)bt;
-
-  auto tile_start = [&](int k) { return seg_start + kTile * (ph + P * k); };
-
+  const __attribute__((address_space(4))) int* btc;
+  int hkv, r, c, bs;
+  uint32_t row_elems, row_bytes;  // elements (bytes) between slots
+  const uint16_t* kbase;
+  const uint16_t* vbase;
   // Per-lane byte offsets of the tile's K/V loads from its first slot's
   // kv-head row: load j reads token 4j + r, dims [8c, 8c + 8). A block's
   // bytes fit 32 bits (checked at launch), so each load is a uniform 64-bit
   // base plus one of these fixed 32-bit lane offsets.
-  const uint32_t row_bytes = row_elems * 2u;
   uint32_t loff[kLoads];
-#pragma unroll
-  for (int j = 0; j < kLoads; ++j) loff[j] = (uint32_t)(4 * j + r) * row_bytes + 16u * c;
 
-  // Issue the K and V loads of this wave's tile k. Tokens at or past seg_end
-  // read the tile's first token instead (always valid), so no load touches an
-  // unallocated block or a tail slot; their scores are masked in consume().
-  auto issue = [&](int k, TileRegs& t) {
-    const int ts = tile_start(k);
+  __device__ __forceinline__ ValuTiles(const ScanArgs& a_, const int* bt_, int hkv_, int r_, int c_)
+      : a(a_),
+        bt(bt_),
+        btc((const __attribute__((address_space(4))) int*)bt_),
+        hkv(hkv_),
+        r(r_),
+        c(c_),
+        bs(a_.block_size),
+        row_elems((uint32_t)a_.Hkv * kHeadDim),
+        row_bytes((uint32_t)a_.Hkv * kHeadDim * 2u),
+        kbase(a_.k_cache + (size_t)hkv_ * kHeadDim + 8 * c_),
+        vbase(a_.v_cache + (size_t)hkv_ * kHeadDim + 8 * c_) {
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) loff[j] = (uint32_t)(4 * j + r) * row_bytes + 16u * c;
+  }
+
+  __device__ __forceinline__ void issue(int ts, int end, TileRegs& t) const {
     if constexpr (kBlockUniform) {
       // The 16 tokens of the tile share one block: scalar block-id load and a
       // uniform base at the tile's first slot.
@@ -129,7 +123,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
       // the loads made the waits after it conservative (measured: 15% slower).
 #pragma unroll
       for (int j = 0; j < kLoads; ++j) {
-        const uint32_t off = ts + 4 * j + r < seg_end ? loff[j] : 16u * c;
+        const uint32_t off = ts + 4 * j + r < end ? loff[j] : 16u * c;
         t.k[j] = load_kv(kr, off);
         t.v[j] = load_kv(vr, off);
       }
@@ -137,7 +131,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
 #pragma unroll
       for (int j = 0; j < kLoads; ++j) {
         int tok = ts + 4 * j + r;
-        tok = tok < seg_end ? tok : ts;
+        tok = tok < end ? tok : ts;
         const uint32_t lb = fastdiv((uint32_t)tok, a.bs_div);
         const int slot = tok - (int)lb * bs;
         const size_t off = ((size_t)bt[lb] * bs + slot) * row_elems;
@@ -145,14 +139,13 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
         t.v[j] = load_kv(vbase + off);
       }
     }
-  };
+  }
 
-  // Fold tile k into st. kMasked: the tile may reach past seg_end (only a
-  // wave's last tile can, and the steady-state loop never consumes that one);
-  // scores of tokens at or past seg_end become -inf.
-  auto consume = [&](int k, const TileRegs& t, auto masked) {
-    constexpr bool kMasked = decltype(masked)::value;
-    const int ts = tile_start(k);
+  // Fold the tile starting at ts into st. kMasked: the tile may reach past
+  // end; scores of tokens at or past end become -inf.
+  template <bool kMasked>
+  __device__ __forceinline__ void consume(int ts, int end, const uint4 (&qf)[GH], const TileRegs& t,
+                                          WaveState<GH>& st) const {
     float s[kLoads][GH];  // raw scores q.k, then probabilities
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
@@ -163,7 +156,7 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
         d = dot2_bf16(qf[h].z, t.k[j].z, d);
         d = dot2_bf16(qf[h].w, t.k[j].w, d);
         d = row16_sum(d);
-        if constexpr (kMasked) d = ts + 4 * j + r < seg_end ? d : kNegInf;
+        if constexpr (kMasked) d = ts + 4 * j + r < end ? d : kNegInf;
         s[j][h] = d;
       }
     }
@@ -210,6 +203,36 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
 #pragma unroll
         for (int d = 0; d < 8; ++d) st.acc[h][d] = fmaf(s[j][h], vf[d], st.acc[h][d]);
     }
+  }
+};
+
+// Scan tokens [seg_start, seg_end) of kv-head hkv of the request whose block
+// table row is bt: wave ph of the P takes tiles ph, ph + P, ... of the range and
+// folds them into st. DEPTH register tiles are in flight; the steady-state
+// loop issues tile k + DEPTH - 1 before consuming tile k and has no branch, so
+// the wait before each consume covers only the tile being consumed.
+// kPinIssue puts a scheduling barrier after each tile's loads: without it the
+// compiler may sink a tile's loads below the previous tile's arithmetic, so
+// that tile is consumed right after its loads are issued. Measured on MI355X:
+// pinning speeds the token-balanced kernel up ~5% (ragged B=128 batch) and is
+// neutral to 1% slower for the split-rule kernel, whose default schedule
+// already overlaps.
+template <int GH, int P, int DEPTH, bool kBlockUniform, bool kPinIssue = false>
+__device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, int hkv,
+                                             const uint4 (&qf)[GH], int seg_start, int seg_end,
+                                             int ph, int r, int c, WaveState<GH>& st) {
+  // The steady-state loop leaves each wave's last tile (the only one that can
+  // reach past seg_end) to the masked tail only with two or more tiles in
+  // flight.
+  static_assert(DEPTH >= 2, "scan_segment needs at least two tiles in flight");
+  const int ntiles = (seg_end - seg_start + kTile - 1) / kTile;
+  const int my_tiles = ntiles > ph ? (ntiles - ph + P - 1) / P : 0;
+  const ValuTiles<GH, kBlockUniform> tiles(a, bt, hkv, r, c);
+
+  auto tile_start = [&](int k) { return seg_start + kTile * (ph + P * k); };
+  auto issue = [&](int k, TileRegs& t) { tiles.issue(tile_start(k), seg_end, t); };
+  auto consume = [&](int k, const TileRegs& t, auto masked) {
+    tiles.template consume<decltype(masked)::value>(tile_start(k), seg_end, qf, t, st);
   };
   constexpr std::true_type kTail{};
   constexpr std::false_type kFull{};
@@ -249,6 +272,48 @@ __device__ __forceinline__ void scan_segment(const ScanArgs& a, const int* bt, i
   }
 }
 
+// One wave scans tokens [rs, re) of kv-head hkv in consecutive 16-token tiles,
+// where rs is the start of a split and the splits are tps tiles long (tps
+// even: split lengths are multiples of kChunkAlign tokens), and calls
+// flush(st) at the end of each split it scans -- the last one ends at re --
+// which must store the state and re-initialise it. Two tiles are in flight
+// across split boundaries as well, so the loads of a split's first tiles are
+// issued while the previous split's last tile is folded: a wave's splits
+// stream as one segment. Split boundaries fall after odd-numbered tiles only,
+// so the boundary test runs once per pair of tiles.
+template <int GH, bool kBlockUniform, class Flush>
+__device__ __forceinline__ void scan_split_range(const ScanArgs& a, const int* bt, int hkv,
+                                                 const uint4 (&qf)[GH], int rs, int re, int tps,
+                                                 int r, int c, WaveState<GH>& st, Flush&& flush) {
+  const int ntiles = (re - rs + kTile - 1) / kTile;
+  if (ntiles <= 0) return;
+  const ValuTiles<GH, kBlockUniform> tiles(a, bt, hkv, r, c);
+  TileRegs t0, t1;
+  tiles.issue(rs, re, t0);
+  int k = 0, left = tps;
+  for (; k + 2 < ntiles; k += 2) {  // tiles k and k + 1 are whole and not the last
+    const int ts = rs + kTile * k;
+    tiles.issue(ts + kTile, re, t1);
+    tiles.template consume<false>(ts, re, qf, t0, st);
+    tiles.issue(ts + 2 * kTile, re, t0);
+    tiles.template consume<false>(ts + kTile, re, qf, t1, st);
+    left -= 2;
+    if (left == 0) {
+      flush(st);
+      left = tps;
+    }
+  }
+  const int ts = rs + kTile * k;
+  if (k + 1 < ntiles) {
+    tiles.issue(ts + kTile, re, t1);
+    tiles.template consume<true>(ts, re, qf, t0, st);
+    tiles.template consume<true>(ts + kTile, re, qf, t1, st);
+  } else {
+    tiles.template consume<true>(ts, re, qf, t0, st);
+  }
+  flush(st);
+}
+
 // Merge the 4 row states of the wave in place (every row ends with the same
 // totals): Mw / Lw get the wave's max and sum, st.acc the rescaled sums.
 template <int GH>
@@ -256,19 +321,11 @@ __device__ __forceinline__ void merge_rows(WaveState<GH>& st, float (&Mw)[GH], f
 #pragma unroll
   for (int h = 0; h < GH; ++h) {
     const float mr = st.m[h];
-    float M = fmaxf(mr, __shfl_xor(mr, 16, 64));
-    M = fmaxf(M, __shfl_xor(M, 32, 64));
+    const float M = xor32_max(xor16_max(mr));
     const float f = mr == M ? 1.f : exp2_fast(mr - (M == kNegInf ? 0.f : M));
-    float lr = st.l[h] * f;
-    lr += __shfl_xor(lr, 16, 64);
-    lr += __shfl_xor(lr, 32, 64);
+    const float lr = xor32_sum(xor16_sum(st.l[h] * f));
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      float x = st.acc[h][d] * f;
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      st.acc[h][d] = x;
-    }
+    for (int d = 0; d < 8; ++d) st.acc[h][d] = xor32_sum(xor16_sum(st.acc[h][d] * f));
     Mw[h] = M;
     Lw[h] = lr;
   }

@@ -7,7 +7,10 @@
 //           work with its MFMAs?) and from two (does it overlap the other
 //           wave's?);
 //   lds     ds_read_b128 bandwidth per CU from 4 or 8 waves, conflict-free
-//           addresses.
+//           addresses;
+//   lanes   the lane semantics of gfx950's row-exchange instructions
+//           (v_permlane16_swap_b32, v_permlane32_swap_b32), which the decode
+//           kernels' cross-row reductions use (issue_probe_lane_swaps).
 // Each probe is one launch of one workgroup per CU, timed with HIP events
 // (median of 5); wave 0 of workgroup 0 also records the shader clock over its
 // loop (s_memtime against the 100 MHz s_memrealtime). Every access stays
@@ -80,36 +83,67 @@ __global__ __launch_bounds__(kMaxThreads) void lds_kernel(float* out, int iters)
   out[blockIdx.x * blockDim.x + threadIdx.x] = (float)(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
 }
 
+// The first HIP error of a probe run (checked by issue_probe_run at its end).
+hipError_t g_error = hipSuccess;
+void note(hipError_t e) {
+  if (e != hipSuccess && g_error == hipSuccess) g_error = e;
+}
+
 template <typename F>
 float median_ms(F launch) {
   hipEvent_t e0, e1;
-  hipEventCreate(&e0);
-  hipEventCreate(&e1);
+  note(hipEventCreate(&e0));
+  note(hipEventCreate(&e1));
   launch();
-  hipDeviceSynchronize();
+  note(hipDeviceSynchronize());
   std::vector<float> ts;
   for (int r = 0; r < 5; ++r) {
-    hipEventRecord(e0);
+    note(hipEventRecord(e0));
     launch();
-    hipEventRecord(e1);
-    hipEventSynchronize(e1);
+    note(hipEventRecord(e1));
+    note(hipEventSynchronize(e1));
     float ms = 0.f;
-    hipEventElapsedTime(&ms, e0, e1);
+    note(hipEventElapsedTime(&ms, e0, e1));
     ts.push_back(ms);
   }
-  hipEventDestroy(e0);
-  hipEventDestroy(e1);
+  note(hipEventDestroy(e0));
+  note(hipEventDestroy(e1));
   std::sort(ts.begin(), ts.end());
   return ts[2];
 }
 
 double clock_mhz() {
   unsigned long long c[2] = {0, 0};
-  hipMemcpyFromSymbol(c, HIP_SYMBOL(g_clock), sizeof(c));
+  note(hipMemcpyFromSymbol(c, HIP_SYMBOL(g_clock), sizeof(c)));
   return c[1] ? 100.0 * (double)c[0] / (double)c[1] : 0.0;
 }
 
+// One wave, x = lane id: out[0..63] and out[64..127] are the two results of
+// v_permlane16_swap_b32 with x as both operands, out[128..191] and
+// out[192..255] those of v_permlane32_swap_b32.
+__global__ __launch_bounds__(64) void lane_swap_kernel(uint32_t* out) {
+  const uint32_t x = threadIdx.x;
+  const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  out[x] = a[0];
+  out[64 + x] = a[1];
+  out[128 + x] = b[0];
+  out[192 + x] = b[1];
+}
+
 }  // namespace
+
+// Runs lane_swap_kernel once and copies its 256 results to host_out. Returns 0,
+// or -1 on a HIP error.
+extern "C" __attribute__((visibility("default"))) int issue_probe_lane_swaps(uint32_t* host_out) {
+  uint32_t* out = nullptr;
+  if (hipMalloc(&out, 256 * sizeof(uint32_t)) != hipSuccess) return -1;
+  lane_swap_kernel<<<1, 64>>>(out);
+  hipError_t err = hipGetLastError();
+  if (err == hipSuccess) err = hipMemcpy(host_out, out, 256 * sizeof(uint32_t), hipMemcpyDeviceToHost);
+  const hipError_t free_err = hipFree(out);
+  return err == hipSuccess && free_err == hipSuccess ? 0 : -1;
+}
 
 // Runs every probe on `cus` workgroups (one per CU) and writes, per probe,
 // {kind, chains or reads in flight, FMAs per iteration, threads, ms, clock MHz}
@@ -119,6 +153,7 @@ extern "C" __attribute__((visibility("default"))) int issue_probe_run(double* ro
                                                                      int cus, int iters) {
   float* out = nullptr;
   if (hipMalloc(&out, sizeof(float) * (size_t)cus * kMaxThreads) != hipSuccess) return -1;
+  g_error = hipSuccess;
   int n = 0;
   auto put = [&](double kind, double p1, double p2, double thr, double ms, double mhz) {
     if (n >= max_rows) return;
@@ -142,7 +177,7 @@ extern "C" __attribute__((visibility("default"))) int issue_probe_run(double* ro
     const float ms8 = median_ms([&] { lds_kernel<8><<<cus, thr>>>(out, iters); });
     put(1, 8, 0, thr, ms8, 0.0);
   }
-  const hipError_t err = hipGetLastError();
-  hipFree(out);
-  return err == hipSuccess ? n : -1;
+  note(hipGetLastError());
+  note(hipFree(out));
+  return g_error == hipSuccess ? n : -1;
 }

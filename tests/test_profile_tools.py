@@ -133,6 +133,35 @@ def test_issue_probe_rates(gpu, capsys):
 
 
 @pytest.mark.gpu
+def test_lane_swap_semantics(gpu):
+    # The row exchanges the decode kernels' cross-row reductions are built on
+    # (gqa_device.hpp: xor16_pair, xor32_pair): with x = lane id as both
+    # operands, v_permlane16_swap_b32 leaves lane l holding x[l] in one result
+    # and x[l ^ 16] in the other (odd 16-lane rows of the first operand swapped
+    # with even rows of the second), v_permlane32_swap_b32 x[l] and x[l ^ 32]
+    # (upper half of the first operand swapped with the lower half of the
+    # second).
+    import ctypes
+
+    import numpy as np
+
+    import issue_probe
+
+    lib = ctypes.CDLL(issue_probe.LIB)
+    out = np.zeros(256, dtype=np.uint32)
+    assert lib.issue_probe_lane_swaps(out.ctypes.data_as(ctypes.c_void_p)) == 0
+    x = np.arange(64, dtype=np.uint32)
+    odd_row, upper = (x // 16) % 2 == 1, x >= 32
+    np.testing.assert_array_equal(out[:64], np.where(odd_row, x - 16, x))
+    np.testing.assert_array_equal(out[64:128], np.where(odd_row, x, x + 16))
+    np.testing.assert_array_equal(out[128:192], np.where(upper, x - 32, x))
+    np.testing.assert_array_equal(out[192:], np.where(upper, x, x + 32))
+    for a, b, k in ((out[:64], out[64:128], 16), (out[128:192], out[192:], 32)):
+        assert (np.minimum(a, b) == np.minimum(x, x ^ k)).all()
+        assert (np.maximum(a, b) == np.maximum(x, x ^ k)).all()
+
+
+@pytest.mark.gpu
 def test_mla_phase_table(gpu, capsys):
     # The phase table of the MLA_PHASE_TIMING build (when it has been built:
     # build.py --variant phase --define MLA_PHASE_TIMING=1) accounts for the
