@@ -120,6 +120,19 @@ def kernel_name(kernel, group, balanced=False, hkv=8):
     return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
 
 
+def provenance_stamp(kind, lib_path):
+    """Source hashes of the measured path and of the library that ran it
+    (python/provenance.py); warns when the library was built from other
+    sources than the tree holds."""
+    import provenance
+
+    st = provenance.stamp(kind, os.path.abspath(lib_path))
+    if not st["library_matches_sources"]:
+        log(f"WARNING: {os.path.relpath(lib_path, REPO_ROOT)} was built from sources "
+            f"{st['library_source_sha16']}, the tree holds {st['source_sha16']}: rebuild")
+    return st
+
+
 def ramp(torch, step, seconds, warmup):
     """Clock ramp: the GPU takes a few hundred milliseconds of load to reach
     its steady clocks, far longer than a few short steps; run untimed steps
@@ -355,6 +368,7 @@ def main(argv=None):
                      "traffic": traffic},
         "device": props.name, "gcn_arch": props.gcnArchName, "cus": props.multi_processor_count,
         "clocks": cases.gpu_clocks(),
+        "provenance": provenance_stamp("gqa", capi.LIB_PATH),
     }
     if sweep:
         result["sweep_us"] = sweep
@@ -494,6 +508,7 @@ def main_mla(args, dev, props):
                      "traffic": read_traffic(args.config, "mla", "balanced" if balanced else ns)},
         "device": props.name, "gcn_arch": props.gcnArchName, "cus": props.multi_processor_count,
         "clocks": cases.gpu_clocks(),
+        "provenance": provenance_stamp("mla", capi.LIB_PATH),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_mla(args, case, out, lse, S_list, scale, median_us)

@@ -9,8 +9,14 @@ those files (complete grid, % of SoL consistent with the times, best split
 consistent with the sweep, spot checks passed, the H100 extraction matching
 the reference's own anchors); any failure aborts without writing.
 
+Every archived record carries the provenance stamp bench.py and
+run_matrix.py write (python/provenance.py): the hash of the sources of the
+measured path and the hash the library that ran was built from. --check also
+fails when an archived record's stamp differs from the tree's current
+sources, so archived numbers cannot outlive the kernels they measured.
+
   python make_report.py            # regenerate results/REPORT.md
-  python make_report.py --check    # exit 1 if the committed report is stale
+  python make_report.py --check    # exit 1 if the report or any archived record is stale
 """
 
 import argparse
@@ -24,6 +30,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 RESULTS = os.path.join(HERE, "results")
 MATRIX_DIR = os.path.join(RESULTS, "matrix_mi355x")
 BENCH_LINES = os.path.join(RESULTS, "bench_configs.jsonl")
+MLA_LINES = os.path.join(RESULTS, "bench_mla.jsonl")
 H100_CSV = os.path.join(RESULTS, "h100_reference_matrix.csv")
 REPORT = os.path.join(RESULTS, "REPORT.md")
 
@@ -65,6 +72,39 @@ def load_h100(path=H100_CSV):
 def load_bench(path=BENCH_LINES):
     with open(path) as f:
         return [json.loads(ln) for ln in f if ln.strip()]
+
+
+def load_mla(path=MLA_LINES):
+    return load_bench(path)
+
+
+# ---------------------------------------------------------------- provenance
+
+def current_sources():
+    sys.path.insert(0, os.path.join(os.path.dirname(HERE), "python"))
+    import provenance
+    return {kind: provenance.source_hash(kind) for kind in provenance.SOURCES}
+
+
+def stale_records(cells, bench, mla, sources):
+    """Labels of archived records not stamped with the current sources of
+    their path (or measured with a library built from other sources)."""
+    stale = []
+
+    def test(label, rec, kind):
+        p = rec.get("provenance")
+        if not p or p.get("path") != kind or p.get("source_sha16") != sources[kind] \
+                or not p.get("library_matches_sources") or p.get("library_defines"):
+            got = p.get("source_sha16") if p else "no stamp"
+            stale.append(f"{label} ({got}; current {kind} sources {sources[kind]})")
+
+    for (hq, s, b, blk), c in sorted(cells.items()):
+        test(f"matrix cell {hq}x8 S{s} B{b} bs{blk}", c, "gqa")
+    for rec in bench:
+        test(f"bench line {rec['config']['workload'][:2]}", rec, "gqa")
+    for rec in mla:
+        test(f"MLA bench line {rec['config']['workload'].split(':')[0]}", rec, "mla")
+    return stale
 
 
 # ---------------------------------------------------------------- anchors
@@ -239,15 +279,49 @@ def sec_argbest(cells):
     return lines
 
 
-def render(cells, h100, bench):
+def sec_mla(mla):
+    lines = ["## K2 MLA absorbed decode (`bench.py --config mla_*`, one MI355X)", "",
+             "Source: `" + rel(MLA_LINES) + "`. FlashMLA's accounting (its benchmark's "
+             "FLOPs and bytes); H100 column: the reference's FlashMLA log on H100 SXM.", "",
+             "| row | causal | launch | median (us) | TFLOP/s | GB/s | % of MFMA peak "
+             "| % of HBM peak | FlashMLA H100 (us) |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for r in mla:
+        cfg = r["config"]
+        h100 = r.get("flashmla_h100_us")
+        lines.append(
+            f"| {cfg['workload'].split(':')[0]} | {'yes' if cfg.get('causal') else 'no'} "
+            f"| {cfg.get('launch', '')} | {r['value']:.1f} | {r['tflops']:.1f} | {r['gbps']:.1f} "
+            f"| {r['roofline']['mfma_frac'] * 100:.1f} | {r['roofline']['hbm_frac'] * 100:.1f} "
+            f"| {h100:.1f} |" if h100 else "| - |")
+    return lines
+
+
+def sec_provenance(cells, bench, mla):
+    def hashes(recs):
+        return sorted({r.get("provenance", {}).get("source_sha16", "none") for r in recs})
+    return ["## Provenance", "",
+            "Every archived record is stamped with the hash of the sources of its path "
+            "(`mla-decode-kernels_amd/python/provenance.py`); `make_report.py --check` fails "
+            "when a stamp differs from the tree.", "",
+            f"- GQA matrix cells: sources {', '.join(hashes(cells.values()))}",
+            f"- GQA bench lines (c1-c5): sources {', '.join(hashes(bench))}",
+            f"- MLA bench lines: sources {', '.join(hashes(mla))}"]
+
+
+def render(cells, h100, bench, mla=()):
     out = ["# MI355X results: GQA paged decode", "",
            "Generated by `mla-decode-kernels_amd/bench/make_report.py` from archived result "
            "files; do not edit by hand. Times are medians in microseconds; % of SoL is KV bytes "
            "/ 8 TB/s over the median. SDPA is torch's AOTriton attention on the same inputs "
            "gathered to contiguous K/V beforehand (its run() timed only). H100 columns are the "
            "reference's published matrix (H100 SXM, 3.35 TB/s).", ""]
-    for sec in (sec_headline(bench, cells, h100), sec_summary(cells),
-                sec_pershape(cells, h100, 16), sec_pershape(cells, h100, 64), sec_argbest(cells)):
+    sections = [sec_headline(bench, cells, h100), sec_summary(cells),
+                sec_pershape(cells, h100, 16), sec_pershape(cells, h100, 64), sec_argbest(cells)]
+    if mla:
+        sections.append(sec_mla(mla))
+    sections.append(sec_provenance(cells, bench, mla))
+    for sec in sections:
         out += sec + [""]
     return "\n".join(out)
 
@@ -257,10 +331,16 @@ def main(argv=None):
     ap.add_argument("--check", action="store_true",
                     help="regenerate in memory; exit 1 if the committed report is stale")
     args = ap.parse_args(argv)
-    cells, h100, bench = load_cells(), load_h100(), load_bench()
+    cells, h100, bench, mla = load_cells(), load_h100(), load_bench(), load_mla()
     sanity(cells, h100, bench)
-    text = render(cells, h100, bench)
+    text = render(cells, h100, bench, mla)
     if args.check:
+        stale = stale_records(cells, bench, mla, current_sources())
+        if stale:
+            print(f"STALE ARCHIVE: {len(stale)} records were not measured on the current sources:")
+            for label in stale[:20]:
+                print(f"  {label}")
+            sys.exit(1)
         try:
             with open(REPORT) as f:
                 same = f.read() == text
@@ -269,7 +349,8 @@ def main(argv=None):
         if not same:
             print(f"STALE: {rel(REPORT)} does not match the archived data")
             sys.exit(1)
-        print("check OK: the report matches the archived data")
+        print("check OK: the report matches the archived data, all stamped with the current "
+              "sources")
         return
     with open(REPORT, "w") as f:
         f.write(text)

@@ -9,6 +9,7 @@ same counters on a plain 1 GiB copy (bench.py --copy-probe 1024).
 
     python profile_config.py --config c5 --out-dir <dir>          # run + summarize
     python profile_config.py --summarize <dir> [--config c5]      # summarize only
+    ... --profile-md profiles/<name>.md   # also write the complete profile file
 
 Passes (each counter set within one rocprofv3 pass's hardware limits):
   trace   --kernel-trace --stats over a 50-step bench run
@@ -75,6 +76,10 @@ SHORT_RUN = ["--steps", "3", "--warmup", "1", "--ramp-seconds", "0", "--no-cpu-b
 
 
 def bench_args(pass_name, config, extra=()):
+    extra = list(extra)
+    if "--lib" in extra:  # the passes run from /tmp: a library path is taken from the repo root
+        i = extra.index("--lib") + 1
+        extra[i] = os.path.join(REPO_ROOT, extra[i])
     if pass_name.startswith("copy_"):
         return ["--copy-probe", "1024"]
     if pass_name == "trace":
@@ -209,6 +214,23 @@ def calibration(root):
     return COPY_BYTES / next(iter(f.values())), COPY_BYTES / next(iter(w.values()))
 
 
+def coalescing(counters, cal):
+    """[(kernel, HBM bytes fetched, VMEM read instructions, bytes per
+    instruction, L2 hit rate or None)] for kernels with both counters."""
+    if not cal:
+        return []
+    rows = []
+    for (k, c), v in sorted(counters.items()):
+        insts = counters.get((k, "SQ_INSTS_VMEM_RD"))
+        if c != "FETCH_SIZE" or not insts:
+            continue
+        fetched = v * cal[0]
+        hit, miss = counters.get((k, "TCC_HIT_sum")), counters.get((k, "TCC_MISS_sum"))
+        rate = hit / (hit + miss) if hit is not None and miss is not None and hit + miss else None
+        rows.append((k, fetched, insts, fetched / insts, rate))
+    return rows
+
+
 def summarize(root):
     lines = []
     dur = kernel_durations(os.path.join(root, "trace"))
@@ -252,6 +274,18 @@ def summarize(root):
                          f"{limits.get('VGPRs', '-')} | {limits.get('LDS', '-')} | "
                          f"{limits['grid']:.2f} | {limiter} |")
     cal = calibration(root)
+    coal = coalescing(counters, cal)
+    if coal:
+        lines += ["", "Coalescing (the counterpart of the reference extractor's sectors per request "
+                  "and L2 bytes, analysis/ncu/extract.py:127-133): HBM bytes fetched (FETCH_SIZE, "
+                  "calibrated) per wave-level vector-memory read instruction "
+                  "(SQ_INSTS_VMEM_RD), next to the L2 hit rate. A wave's 16-byte-per-lane load "
+                  "moves 1024 B when fully coalesced.", "",
+                  "| kernel | HBM bytes fetched | VMEM read instructions | bytes per read "
+                  "instruction | L2 hit |", "|---|---|---|---|---|"]
+        for k, fetched, insts, per, hit in coal:
+            lines.append(f"| {k} | {fetched:,.0f} | {insts:,.0f} | {per:,.0f} | "
+                         + (f"{hit:.1%}" if hit is not None else "-") + " |")
     traffic = None
     if cal and dur:
         dominant = max(dur, key=lambda k: sum(dur[k]))
@@ -280,6 +314,110 @@ def traffic_line(root, config, traffic):
     return f"{config} {kernel} {split} {traffic[0]} {traffic[1]}" if split is not None else None
 
 
+def bench_line(root):
+    """The JSON line bench.py printed in the trace pass, or None."""
+    for f in glob.glob(os.path.join(root, "trace.log")):
+        for line in open(f):
+            if line.startswith("{") and '"metric"' in line:
+                return json.loads(line)
+    return None
+
+
+def build_command(bench_args):
+    """The build.py command that makes the variant library a --lib bench
+    argument names (its defines from the library's provenance record), or
+    None for the shipped library."""
+    parts = bench_args.split()
+    if "--lib" not in parts:
+        return None
+    lib = parts[parts.index("--lib") + 1]
+    sys.path.insert(0, os.path.join(os.path.dirname(HERE), "python"))
+    import provenance
+
+    defines = provenance.library_defines(os.path.join(REPO_ROOT, lib)) or []
+    name = os.path.basename(os.path.dirname(lib))
+    return " ".join(["python mla-decode-kernels_amd/build.py --variant", name] +
+                    [f"--define {d}" for d in defines])
+
+
+def profile_markdown(root, config, argv, summary, build=None):
+    """A complete profiles/*.md: what ran, the command that made it, the
+    traced run's bench line, then the summary tables."""
+    b = bench_line(root) or {}
+    occ = occupancy_rows(os.path.join(root, "trace"))
+    dur = kernel_durations(os.path.join(root, "trace"))
+    dominant = max(dur, key=lambda k: sum(dur[k])) if dur else "?"
+    cfg = b.get("config", {})
+    title = f"# {dominant.split('::')[-1].split('<')[0]} -- config {config}: " \
+            f"{cfg.get('workload', config).split(': ', 1)[-1]}"
+    out = [title, ""]
+    desc = [f"MI355X ({b.get('gcn_arch', 'gfx950')}, {b.get('cus', '?')} CUs), one GPU."]
+    launch = cfg.get("num_splits", cfg.get("launch"))
+    if launch is not None:
+        what = cfg.get("kernel", "MLA decode")
+        how = f"at {launch} split{'s' if launch != 1 else ''}" if isinstance(launch, int) \
+            else f"({launch})"
+        desc.append(f"Launch: {what} {how}.")
+    lib = b.get("provenance", {}).get("library_defines")
+    if lib:
+        desc.append(f"Library: a profiling build with {', '.join(lib)}.")
+    r = occ.get(dominant)
+    if r:
+        g = [int(r[f"Grid_Size_{a}"]) for a in "XYZ"]
+        w = [int(r[f"Workgroup_Size_{a}"]) for a in "XYZ"]
+        threads = w[0] * w[1] * w[2]
+        wgs = (g[0] // w[0]) * (g[1] // w[1]) * (g[2] // w[2])
+        desc.append(f"Dominant kernel {dominant}: {wgs} workgroups of {threads} threads "
+                    f"({wgs * -(-threads // 64)} waves).")
+    if "kv_bytes" in b:
+        desc.append(f"Algorithmic bytes per launch: {b['kv_bytes']:,} (K + V rows, 512 B per "
+                    "(token, kv-head)).")
+    elif "bytes" in b:
+        desc.append(f"Algorithmic bytes per step: {b['bytes']:,.0f} and FLOPs {b['flops']:,.0f} "
+                    "(FlashMLA's accounting).")
+    desc.append("The copy passes calibrate FETCH_SIZE and WRITE_SIZE on a plain 1 GiB copy "
+                "(`bench.py --copy-probe 1024`).")
+    out += [" ".join(desc), "",
+            "Command (from the repository root; one rocprofv3 process per pass, run from /tmp "
+            "with TMPDIR=/tmp, the program after `--` being `python bench.py ...`; the script's "
+            "docstring lists each pass's counters; `<dir>` is any absolute output directory):",
+            "", "    " + (build + " && " if build else "") +
+            "python mla-decode-kernels_amd/bench/profile_config.py " + " ".join(
+                a if " " not in a else f'"{a}"' for a in argv), ""]
+    if b:
+        rl = b.get("roofline", {})
+        prov = b.get("provenance", {})
+        out += [f"Bench line of the traced run: median step {b.get('value')} us, dominant kernel "
+                f"average {rl.get('avg_kernel_us')} us over its back-to-back launches (HIP events "
+                f"on the launch stream), roofline.frac {rl.get('frac')}; sources "
+                f"{prov.get('source_sha16')} ({prov.get('path')} path, "
+                f"mla-decode-kernels_amd/python/provenance.py).", ""]
+    out += ["## Kernel trace, counters, wave-cycle breakdown, occupancy and coalescing "
+            "(per dispatch)", "", summary, ""]
+    return "\n".join(out)
+
+
+TRAFFIC_FILE = os.path.join(REPO_ROOT, "profiles", "traffic.txt")
+
+
+def update_traffic(path, line):
+    """Replace the line with the same config, kernel and split label (the
+    first three fields), or append it; comment lines are kept."""
+    key = line.split()[:3]
+    kept, replaced = [], False
+    for ln in open(path).read().splitlines():
+        if not ln.startswith("#") and ln.split()[:3] == key:
+            if not replaced:
+                kept.append(line)
+                replaced = True
+            continue
+        kept.append(ln)
+    if not replaced:
+        kept.append(line)
+    with open(path, "w") as f:
+        f.write("\n".join(kept) + "\n")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--config", default="c2",
@@ -290,6 +428,11 @@ def main(argv=None):
     ap.add_argument("--summarize", default=None, help="only summarize an existing output dir")
     ap.add_argument("--bench-args", default="",
                     help="extra bench.py arguments for every pass but the copies")
+    ap.add_argument("--profile-md", default=None,
+                    help="also write the complete profile file (header, command, tables) here")
+    ap.add_argument("--update-traffic", action="store_true",
+                    help="replace (or add) this run's line in profiles/traffic.txt, which "
+                         "bench.py reads for roofline.traffic")
     args = ap.parse_args(argv)
     root = args.summarize or args.out_dir
     if root is None:
@@ -301,10 +444,23 @@ def main(argv=None):
     with open(os.path.join(root, "summary.md"), "w") as f:
         f.write(text + "\n")
     print(text)
+    if args.profile_md:
+        shown = ["--config", args.config, "--out-dir", "<dir>"]
+        if args.passes != ",".join(PASSES):
+            shown += ["--passes", args.passes]
+        if args.bench_args:
+            shown += ["--bench-args", args.bench_args]
+        shown += ["--profile-md", os.path.relpath(os.path.abspath(args.profile_md), REPO_ROOT)]
+        with open(args.profile_md, "w") as f:
+            f.write(profile_markdown(root, args.config, shown, text, build_command(args.bench_args)))
+        print(f"wrote {args.profile_md}")
     if traffic:
         line = traffic_line(root, args.config, traffic)
         if line:
             print("traffic line:", line)
+            if args.update_traffic:
+                update_traffic(TRAFFIC_FILE, line)
+                print(f"updated {os.path.relpath(TRAFFIC_FILE, REPO_ROOT)}")
 
 
 if __name__ == "__main__":

@@ -24,9 +24,10 @@ pool of 1.1x the needed blocks):
 
 The baseline is torch SDPA on AOTriton over pages gathered into contiguous
 K/V at plan time (baselines/sdpa_adapter.py); with --baseline none it is
-skipped. Each cell writes its own JSON into --out-dir and is skipped when that
-file exists, so an interrupted run resumes; matrix_summary.csv is rebuilt
-from all cell files at the end.
+skipped. Each cell record is a JSON file in --out-dir (MatrixDir) stamped with
+the provenance of the library that ran it (python/provenance.py); cells whose
+file exists are not run again, so an interrupted run resumes, and
+matrix_summary.csv is rebuilt from all cell files at the end.
 """
 
 import argparse
@@ -45,8 +46,11 @@ sys.path.insert(0, _HERE)
 sys.path.insert(0, os.path.join(os.path.dirname(_HERE), "python"))
 
 import cases  # noqa: E402
+import provenance  # noqa: E402
 from binding import (KERNELS, gqa_decode_balanced, gqa_decode_v2,  # noqa: E402
                      num_splits_heuristic, prefer_balanced)
+
+KERNEL_LIB = os.path.join(os.path.dirname(_HERE), "lib", "libgqa_decode_hip.so")
 
 HEADTYPES = [(32, 8), (64, 8)]
 S_LIST = [512, 2048, 8192, 32768]
@@ -157,43 +161,83 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus, warmup=None, runs=None):
         "spot_check": {k: f"passed (max-abs {v:.3e})" for k, v in checks.items()},
         "baseline": baseline,
         "clocks": cases.gpu_clocks(),
+        "provenance": provenance.stamp("gqa", KERNEL_LIB),
         "results": results,
     }
 
 
-def write_summary(out_dir):
-    """matrix_summary.csv from every cell file: the reference's columns
-    (headtype .. pct_of_sol, then the speed ratio against the cell's baseline,
-    named after it as the reference's ratio_vs_flashinfer is), plus `choice`,
-    the automatic launch's recorded choice."""
-    rows = []
-    for fname in sorted(os.listdir(out_dir)):
-        if not (fname.startswith("cell_") and fname.endswith(".json")):
-            continue
-        with open(os.path.join(out_dir, fname)) as f:
-            cell = json.load(f)
-        baseline = cell.get("baseline", "none")
-        base = cell["results"].get(baseline, {}).get("median_ms")
-        for kernel, r in cell["results"].items():
-            rows.append({
-                "headtype": f"{cell['Hq']}x{cell['Hkv']}",
-                "S": cell["S"], "B": cell["B"], "block": cell["block"],
-                "kernel": kernel,
-                "best_splits": r.get("best_splits", ""),
-                "median_ms": r["median_ms"],
-                "pct_of_sol": r["pct_of_sol"],
-                # > 1: faster than the baseline
-                f"ratio_vs_{baseline}": base / r["median_ms"] if base else "",
-                "choice": r.get("choice", ""),
-            })
-    if not rows:
-        return
-    path = os.path.join(out_dir, "matrix_summary.csv")
-    with open(path, "w", newline="") as f:
-        w = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
-        w.writeheader()
-        w.writerows(rows)
-    print(f"wrote {path} ({len(rows)} rows)", flush=True)
+# matrix_summary.csv: the reference's columns (headtype .. pct_of_sol), then
+# the speed ratio against the cell's baseline (named after it, as the
+# reference's ratio_vs_flashinfer is; > 1 is faster than the baseline) and the
+# automatic launch's recorded choice.
+SUMMARY_COLUMNS = ["headtype", "S", "B", "block", "kernel", "best_splits", "median_ms",
+                   "pct_of_sol"]
+
+
+def summary_rows(cell):
+    """One summary row per timed variant of a cell record, in column order."""
+    base = cell["results"].get(cell.get("baseline", "none"), {}).get("median_ms")
+    for kernel, r in cell["results"].items():
+        yield [f"{cell['Hq']}x{cell['Hkv']}", cell["S"], cell["B"], cell["block"], kernel,
+               r.get("best_splits", ""), r["median_ms"], r["pct_of_sol"],
+               base / r["median_ms"] if base else "", r.get("choice", "")]
+
+
+class MatrixDir:
+    """A matrix run's directory: one JSON record per finished cell, written
+    whole (temporary file, then rename) so a killed run never leaves half a
+    record, and the summary CSV rebuilt from whatever records exist."""
+
+    def __init__(self, path):
+        self.path = path
+        os.makedirs(path, exist_ok=True)
+
+    def record_path(self, cell):
+        return os.path.join(self.path, f"{cell_name(*cell)}.json")
+
+    def has(self, cell):
+        return os.path.exists(self.record_path(cell))
+
+    def save(self, cell, record):
+        tmp = self.record_path(cell) + ".tmp"
+        with open(tmp, "w") as f:
+            json.dump(record, f, indent=2)
+        os.replace(tmp, self.record_path(cell))
+
+    def records(self):
+        """The finished cells' records, in grid order."""
+        for cell in all_cells():
+            if self.has(cell):
+                with open(self.record_path(cell)) as f:
+                    yield json.load(f)
+
+    def write_summary(self):
+        records = list(self.records())
+        if not records:
+            return
+        baseline = records[0].get("baseline", "none")
+        path = os.path.join(self.path, "matrix_summary.csv")
+        with open(path, "w", newline="") as f:
+            w = csv.writer(f)
+            w.writerow(SUMMARY_COLUMNS + [f"ratio_vs_{baseline}", "choice"])
+            n = 0
+            for rec in records:
+                for row in summary_rows(rec):
+                    w.writerow(row)
+                    n += 1
+        print(f"wrote {path} ({n} rows)", flush=True)
+
+
+def describe(record, baseline):
+    """One progress line's worth of a finished cell."""
+    r = record["results"]
+    auto = r["v2_auto"]
+    text = (f"v2 best {r['v2']['median_ms'] * 1e3:.1f} us (ns={r['v2']['best_splits']}), "
+            f"automatic {auto['median_ms'] * 1e3:.1f} us ({auto['choice']}, "
+            f"{auto['pct_of_sol']:.1f}% SoL)")
+    if baseline in r:
+        text += f", {baseline} {r[baseline]['median_ms'] * 1e3:.1f} us"
+    return text
 
 
 def main(argv=None):
@@ -210,44 +254,30 @@ def main(argv=None):
                          "S=32768 with B>=32)")
     args = ap.parse_args(argv)
 
-    out_dir = args.out_dir or os.path.join(_HERE, "results",
-                                           time.strftime("matrix_%Y%m%d_%H%M%S"))
-    os.makedirs(out_dir, exist_ok=True)
-    print(f"matrix output dir: {out_dir}", flush=True)
-
-    cells = all_cells()
+    mdir = MatrixDir(args.out_dir or os.path.join(_HERE, "results",
+                                                  time.strftime("matrix_%Y%m%d_%H%M%S")))
+    print(f"matrix output dir: {mdir.path}", flush=True)
+    grid = all_cells()
     if args.only:
         keys = args.only.split(",")
-        cells = [c for c in cells if any(k in cell_name(*c) for k in keys)]
-    memory_precheck(cells, args.baseline != "none")
+        grid = [c for c in grid if any(k in cell_name(*c) for k in keys)]
+    todo = [c for c in grid if not mdir.has(c)]
+    print(f"{len(grid) - len(todo)} of {len(grid)} cells already recorded (kept, not rerun); "
+          f"{len(todo)} to run", flush=True)
+    if todo:
+        memory_precheck(todo, args.baseline != "none")
     num_cus = torch.cuda.get_device_properties(0).multi_processor_count
 
-    durations = []
-    for i, c in enumerate(cells, 1):
-        name = cell_name(*c)
-        path = os.path.join(out_dir, f"{name}.json")
-        if os.path.exists(path):
-            print(f"[{i}/{len(cells)}] {name}: exists, skipping", flush=True)
-            continue
-        print(f"[{i}/{len(cells)}] {name}: running", flush=True)
-        t0 = time.time()
-        cell = run_cell(*c, args.baseline, num_cus, warmup=args.warmup, runs=args.runs)
-        with open(path, "w") as f:
-            json.dump(cell, f, indent=2)
+    t_start = time.time()
+    for done, cell in enumerate(todo, 1):
+        print(f"[{done}/{len(todo)}] {cell_name(*cell)}: running", flush=True)
+        record = run_cell(*cell, args.baseline, num_cus, warmup=args.warmup, runs=args.runs)
+        mdir.save(cell, record)
         torch.cuda.empty_cache()
-        dt = time.time() - t0
-        durations.append(dt)
-        r = cell["results"]
-        base = f" {args.baseline} {r[args.baseline]['median_ms'] * 1e3:.1f} us" \
-            if args.baseline in r else ""
-        print(f"[{i}/{len(cells)}] {name}: done in {dt:.1f}s; v2 best "
-              f"{r['v2']['median_ms'] * 1e3:.1f} us (ns={r['v2']['best_splits']}), automatic "
-              f"{r['v2_auto']['median_ms'] * 1e3:.1f} us ({r['v2_auto']['choice']}, "
-              f"{r['v2_auto']['pct_of_sol']:.1f}% SoL){base}; "
-              f"~{(len(cells) - i) * sum(durations) / len(durations) / 60:.1f} min left",
-              flush=True)
-
-    write_summary(out_dir)
+        left = (time.time() - t_start) / done * (len(todo) - done) / 60
+        print(f"[{done}/{len(todo)}] {cell_name(*cell)}: {describe(record, args.baseline)}; "
+              f"~{left:.1f} min left", flush=True)
+    mdir.write_summary()
 
 
 if __name__ == "__main__":

@@ -8,11 +8,17 @@
 
 Products (in-tree, git-ignored, shipped with the source tree):
   lib/libgqa_decode_hip.so   hipcc --offload-arch=gfx950: every kernel + the C ABI
+                             (+ .sources.json: the source hashes it was built
+                             from, python/provenance.py)
   lib/gqa_decode_ext*.so     g++: host-only torch operator layer linking the above
   lib/libgqa_stream_probe.so hipcc: the streaming-read probe bench.py measures
                              the bandwidth ceiling with (not on the decode path)
-  lib/libissue_probe.so      hipcc: MFMA / VALU / LDS issue-rate probes
-                             (bench/issue_probe.py; not on the decode path)
+  lib/libissue_probe.so      hipcc: MFMA / VALU / LDS issue-rate probes and the
+                             lane-swap probe (bench/issue_probe.py,
+                             tests/test_profile_tools.py; not on the decode path)
+  _build/phase/libgqa_decode_hip.so
+                             the kernel library built with MLA_PHASE_TIMING=1
+                             (bench/mla_phases.py; not on the decode path)
 
 The extension is compiled as plain C++ (no .cu/.hip source, so torch's
 hipify pass never runs); it reaches the GPU only through the C ABI.
@@ -25,6 +31,7 @@ import subprocess
 import sys
 import sysconfig
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_ROOT = os.path.dirname(PKG_DIR)
@@ -35,6 +42,10 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 KERNEL_LIB = os.path.join(LIB_DIR, "libgqa_decode_hip.so")
+# The MLA decode's phase-timing build (bench/mla_phases.py reads its table).
+PHASE_LIB = os.path.join(PKG_DIR, "_build", "phase", "libgqa_decode_hip.so")
+PHASE_DEFINES = ["MLA_PHASE_TIMING=1"]
+OBJ_DIR = os.path.join(PKG_DIR, "_build", "obj")  # objects: not shipped to GPU runs
 PROBE_LIB = os.path.join(LIB_DIR, "libgqa_stream_probe.so")
 ISSUE_PROBE_LIB = os.path.join(LIB_DIR, "libissue_probe.so")
 HIP_SOURCES = ["gqa_decode_v0.hip", "gqa_decode_split.hip", "gqa_decode_mfma.hip",
@@ -62,14 +73,28 @@ def _run(cmd, cwd=None):
 
 
 def build_kernels(out=KERNEL_LIB, defines=()):
+    """hipcc every HIP source to an object (in parallel), then link them into
+    the shared library `out`, with the source hashes next to it."""
     os.makedirs(os.path.dirname(out), exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    tmp = out + ".tmp"
     flags = [f"-D{d}" for d in defines]
-    dt = _run([hipcc, *HIP_FLAGS, *flags, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    tag = os.path.relpath(out, PKG_DIR).replace(os.sep, "_")
+    objdir = os.path.join(OBJ_DIR, tag)
+    os.makedirs(objdir, exist_ok=True)
+    t0 = time.time()
+    objs = [os.path.join(objdir, os.path.splitext(src)[0] + ".o") for src in HIP_SOURCES]
+    with ThreadPoolExecutor(max_workers=len(HIP_SOURCES)) as pool:
+        list(pool.map(lambda so: _run([hipcc, *HIP_FLAGS, *flags, f"-I{INCLUDE}", "-c",
+                                       os.path.join(CSRC, so[0]), "-o", so[1]]),
+                      zip(HIP_SOURCES, objs)))
+    tmp = out + ".tmp"
+    _run([hipcc, *HIP_FLAGS, "-shared", *objs, "-o", tmp])
     os.replace(tmp, out)
-    print(f"built {os.path.relpath(out, REPO_ROOT)} in {dt:.1f}s")
+    # The source hashes this library was built from (results carry them).
+    sys.path.insert(0, os.path.join(PKG_DIR, "python"))
+    import provenance
+    provenance.write_sidecar(out, defines)
+    print(f"built {os.path.relpath(out, REPO_ROOT)} in {time.time() - t0:.1f}s")
     return out
 
 
@@ -133,6 +158,7 @@ def main(argv=None):
                       args.define)
         return
     build_kernels()
+    build_kernels(PHASE_LIB, PHASE_DEFINES)
     build_probe()
     build_probe("issue_probe.hip", ISSUE_PROBE_LIB)
     if not args.no_ext:

@@ -10,9 +10,10 @@ all passed); the cell record carries the reference's keys
 (bench/run_matrix.py:121-128 of the reference) with consistent values -- the
 KV bytes and SoL of the cell, pct_of_sol = sol_ms / median_ms * 100 for every
 variant, the best split count the argmin of the sweep; v0 is timed because
-S <= 2048 and B <= 8; the CSV holds the reference's columns
+S <= 2048 and B <= 8; the record is stamped with the library's provenance,
+matching the tree's sources; the CSV holds the reference's columns
 (bench/run_matrix.py:117-124) and one row per variant; and a second run
-resumes (skips the existing cell)."""
+resumes (keeps the existing cell)."""
 
 import csv
 import json
@@ -44,6 +45,8 @@ def test_matrix_cell_end_to_end(gpu, tmp_path, capsys):
     Hq, Hkv, S, B, bs = CELL
     assert (cell["Hq"], cell["Hkv"], cell["S"], cell["B"], cell["block"]) == CELL
     assert (cell["warmup"], cell["runs"]) == (2, 5)
+    assert cell["provenance"]["path"] == "gqa"
+    assert cell["provenance"]["library_matches_sources"], cell["provenance"]
     assert cell["kv_bytes"] == S * B * Hkv * 128 * 2 * 2
     assert cell["sol_ms"] == pytest.approx(cell["kv_bytes"] / cases.HBM_PEAK_BYTES_PER_S * 1e3)
 
@@ -81,5 +84,5 @@ def test_matrix_cell_end_to_end(gpu, tmp_path, capsys):
     mtime = os.path.getmtime(path)
     capsys.readouterr()
     run_matrix.main(argv)
-    assert "exists, skipping" in capsys.readouterr().out
+    assert "1 of 1 cells already recorded" in capsys.readouterr().out
     assert os.path.getmtime(path) == mtime

@@ -63,6 +63,10 @@ def test_summarize(tmp_path):
     counters("copy_write", neg, "WRITE_SIZE", [1048576])
     counters("fetch", scan, "FETCH_SIZE", [1000, 1002])
     counters("write", scan, "WRITE_SIZE", [8])
+    counters("lds", scan, "SQ_INSTS_VMEM_RD", [2002])
+    write_csv(os.path.join(root, "l2", "x", "run_counter_collection.csv"),
+              [dict(Kernel_Name=scan, Counter_Name="TCC_HIT_sum", Counter_Value=1),
+               dict(Kernel_Name=scan, Counter_Name="TCC_MISS_sum", Counter_Value=3)])
     with open(os.path.join(root, "trace.log"), "w") as f:
         f.write("progress line\n" + json.dumps({"metric": "m", "config": {"num_splits": "balanced"}})
                 + "\n")
@@ -73,6 +77,13 @@ def test_summarize(tmp_path):
     # 2^30 bytes per 524288 units = 2048 B per FETCH unit, 1024 per WRITE unit.
     assert traffic == (1001 * 2048, 8 * 1024)
     assert pc.traffic_line(root, "c5", traffic) == f"c5 v2 balanced {1001 * 2048} {8 * 1024}"
+    # Coalescing: 1001 x 2048 bytes over 2002 read instructions = 1024 B each;
+    # L2 hit 1 of 4.
+    assert "| gqa::gqa_decode_balanced_kernel<4, 4, 2, true> | 2,050,048 | 2,002 | 1,024 | 25.0% |" \
+        in text
+    md = pc.profile_markdown(root, "c5", ["--config", "c5", "--out-dir", "<dir>"], text)
+    assert md.startswith("# gqa_decode_balanced_kernel -- config c5")
+    assert "profile_config.py --config c5 --out-dir <dir>" in md and text in md
 
 
 def test_short_name_drops_signature_and_anonymous_namespace():
@@ -163,12 +174,15 @@ def test_lane_swap_semantics(gpu):
 
 @pytest.mark.gpu
 def test_mla_phase_table(gpu, capsys):
-    # The phase table of the MLA_PHASE_TIMING build (when it has been built:
-    # build.py --variant phase --define MLA_PHASE_TIMING=1) accounts for the
-    # whole kernel: phases within a few percent of the wave's cycles.
+    # The phase table of the MLA_PHASE_TIMING build (build.py makes it with
+    # every build, from the tree's sources) accounts for the whole kernel:
+    # phases within a few percent of the wave's cycles.
+    import provenance
+
     lib = os.path.join(os.path.dirname(pc.HERE), "_build", "phase", "libgqa_decode_hip.so")
-    if not os.path.exists(lib):
-        pytest.skip("profiling build not present (build.py --variant phase --define MLA_PHASE_TIMING=1)")
+    assert os.path.exists(lib), f"{lib} missing: run mla-decode-kernels_amd/build.py"
+    assert provenance.library_hash("mla", lib) == provenance.source_hash("mla"), (
+        "the phase-timing build is stale: rebuild with mla-decode-kernels_amd/build.py")
     import mla_phases
 
     # The process has already loaded the in-tree library (capi.lib(), the
@@ -220,3 +234,11 @@ def test_stream_probe_patterns(gpu, capsys):
         e = res[key]["wg_end_us"]
         assert 0 < e["min"] <= e["p10"] <= e["p50"] <= e["p90"] <= e["max"], (key, e)
         assert e["max"] < 2 * res[key]["median_us"], (key, e, res[key]["median_us"])
+
+
+def test_update_traffic_replaces_or_appends(tmp_path):
+    path = tmp_path / "traffic.txt"
+    path.write_text("# header\nc2 v2 1 10 20\nc3 v2 4 30 40\n")
+    pc.update_traffic(str(path), "c2 v2 1 11 21")
+    pc.update_traffic(str(path), "c5 v2 balanced 50 60")
+    assert path.read_text() == "# header\nc2 v2 1 11 21\nc3 v2 4 30 40\nc5 v2 balanced 50 60\n"
