@@ -259,8 +259,13 @@ GQA_DECODE_API int gqa_decode_balanced_merge_launch(
  * Its workspace is a file-scope device array of
  * GQA_DECODE_NOALLOC_SCRATCH_BYTES in the library, one copy per device
  * (resolved for the stream's device on the first call there, and held until
- * the process ends); the call allocates nothing. Same arguments, kernels and
- * bits as gqa_decode_balanced_launch with the same num_workgroups. Returns
+ * the process ends); the call allocates nothing. num_workgroups <= 0 means the
+ * CU count of the stream's device (the device whose array is used). Same
+ * arguments, kernels and bits as gqa_decode_balanced_launch with the same
+ * num_workgroups. The first call on a device must not be made while the
+ * stream is being captured into a graph (it returns
+ * hipErrorStreamCaptureUnsupported, launching nothing): make one eager call
+ * per device first; later calls can be captured. Returns
  * hipErrorOutOfMemory, launching nothing, when
  * gqa_decode_balanced_workspace_bytes(B, Hq, Hkv, num_workgroups) exceeds
  * GQA_DECODE_NOALLOC_SCRATCH_BYTES; otherwise as gqa_decode_balanced_launch.

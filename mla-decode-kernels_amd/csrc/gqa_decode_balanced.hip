@@ -508,6 +508,18 @@ hipError_t launch_balanced_mfma_merge(const ScanArgs& a, const BalancedArgs& ba,
   return hipGetLastError();
 }
 
+// Groups of at least this many q-heads over 4 or 8 kv-heads take the
+// matrix-core balanced scan: every such group by default. A profiling build
+// with 5 (build.py --variant ... --define GQA_BALANCED_MFMA_MIN_GROUP=5)
+// keeps groups of up to 4 on the VALU balanced scan, the other side of the
+// measurement behind this default.
+#ifndef GQA_BALANCED_MFMA_MIN_GROUP
+#define GQA_BALANCED_MFMA_MIN_GROUP 1
+#endif
+inline bool balanced_mfma(int Hkv, int G) {
+  return mfma_slot_shape(Hkv, G) && G >= GQA_BALANCED_MFMA_MIN_GROUP;
+}
+
 int balanced_workgroups(int num_workgroups) {
   return num_workgroups > 0 ? num_workgroups : device_cu_count();
 }
@@ -522,7 +534,7 @@ extern "C" size_t gqa_decode_balanced_workspace_bytes(int B, int Hq, int Hkv, in
   const int nwg = gqa::balanced_workgroups(num_workgroups);
   if (nwg <= 0) return 0;
   // State slots hold one kv-head's q-heads (VALU scan) or all Hq (MFMA scan).
-  const int slot_heads = gqa::mfma_slot_shape(Hkv, G) ? Hq : gqa::heads_per_wave(G);
+  const int slot_heads = gqa::balanced_mfma(Hkv, G) ? Hq : gqa::heads_per_wave(G);
   return gqa::balanced_states_bytes(nwg, slot_heads) + (size_t)nwg * sizeof(gqa::ShareMeta);
 }
 
@@ -548,7 +560,7 @@ int balanced_launch(BalancedPart part, const uint16_t* q, const uint16_t* k_cach
   // ragged and uniform batches alike (config 5: 1185 vs 1229 us; ragged B=64,
   // 32768 tokens, groups of 1/2/3: 642/644/646 vs 684/688/709 us). Other
   // kv-head counts keep the VALU scan (groups of up to 4).
-  const bool mfma = gqa::mfma_slot_shape(Hkv, G);
+  const bool mfma = gqa::balanced_mfma(Hkv, G);
   if (gqa::use_mfma(G) && !mfma) return hipErrorInvalidValue;
   const int64_t s_cap = (int64_t)max_blocks * block_size;
   // Every tile index of the batch, segs * sum_b ceil(S_b / 16), fits in 31 bits
@@ -652,17 +664,27 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the device `stream` belongs to (the current
-// device for the null stream).
-hipError_t scratch_for_stream(hipStream_t stream, void** ptr) {
-  int cur = 0, dev = 0;
-  hipError_t err = hipGetDevice(&cur);
-  if (err != hipSuccess) return err;
-  dev = cur;
-  if (stream != nullptr && (err = hipStreamGetDevice(stream, &dev)) != hipSuccess) return err;
-  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+// The device `stream` belongs to (the current device for the null stream).
+hipError_t stream_device(hipStream_t stream, int* dev) {
+  hipError_t err = hipGetDevice(dev);
+  if (err == hipSuccess && stream != nullptr) err = hipStreamGetDevice(stream, dev);
+  if (err == hipSuccess && (*dev < 0 || *dev >= kMaxDevices)) err = hipErrorInvalidDevice;
+  return err;
+}
+
+// Device address of `scratch` on device dev, looked up on the first call for
+// that device (with dev current) and kept. The lookup may load the library's
+// code object on that device, which a stream being captured into a graph must
+// not see: a first call while `stream` is capturing is refused.
+hipError_t scratch_for_device(int dev, hipStream_t stream, void** ptr) {
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hipError_t err = hipStreamIsCapturing(stream, &capture);
+    if (err != hipSuccess) return err;
+    if (capture != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+    int cur = 0;
+    if ((err = hipGetDevice(&cur)) != hipSuccess) return err;
     if (dev != cur && (err = hipSetDevice(dev)) != hipSuccess) return err;
     void* p = nullptr;
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -684,6 +706,15 @@ extern "C" int gqa_decode_balanced_launch_noalloc(
     const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int* block_table,
     const int* seq_lens, uint16_t* out, int B, int Hq, int Hkv, int block_size, int max_blocks,
     float scale, int num_workgroups, hipStream_t stream) {
+  // Scratch, workspace size and default workgroup count all come from the
+  // device the stream belongs to.
+  int dev = 0;
+  hipError_t err = stream_device(stream, &dev);
+  if (err != hipSuccess) return err;
+  if (num_workgroups <= 0) {
+    err = hipDeviceGetAttribute(&num_workgroups, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return err;
+  }
   const size_t need = gqa_decode_balanced_workspace_bytes(B, Hq, Hkv, num_workgroups);
   if (need == 0)  // B == 0 (nothing to do) or arguments the launcher rejects
     return balanced_launch(BalancedPart::kBoth, q, k_cache, v_cache, block_table, seq_lens, out,
@@ -691,8 +722,7 @@ extern "C" int gqa_decode_balanced_launch_noalloc(
                            stream);
   if (need > GQA_DECODE_NOALLOC_SCRATCH_BYTES) return hipErrorOutOfMemory;
   void* ws = nullptr;
-  const hipError_t err = scratch_for_stream(stream, &ws);
-  if (err != hipSuccess) return err;
+  if ((err = scratch_for_device(dev, stream, &ws)) != hipSuccess) return err;
   return balanced_launch(BalancedPart::kBoth, q, k_cache, v_cache, block_table, seq_lens, out, B,
                          Hq, Hkv, block_size, max_blocks, scale, num_workgroups,
                          static_cast<float*>(ws), GQA_DECODE_NOALLOC_SCRATCH_BYTES, stream);
@@ -744,7 +774,7 @@ extern "C" int gqa_decode_prefer_balanced(int B, int Hq, int Hkv, int block_size
     return B >= kMfmaMinBatch && kv_bytes >= kMfmaMinBytes ? 1 : 0;
   }
   if ((int64_t)Hkv * B * ((s_cap + gqa::kTile - 1) / gqa::kTile) >= (int64_t(1) << 31)) return 0;
-  if (gqa::mfma_slot_shape(Hkv, G) && B < kMfmaMinBatch) return 0;
+  if (gqa::balanced_mfma(Hkv, G) && B < kMfmaMinBatch) return 0;
   if (s_cap < kMinLongest || kv_bytes < kMinBytes) return 0;
   if ((int64_t)B * Hkv > (int64_t)kMaxSegmentsPerCu * num_cus) return 0;
   const int ns = gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus);

@@ -472,9 +472,12 @@ hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_
   a.counters = counters;
   a.merge_out = counters ? merge_out : nullptr;  // the single-launch mode's output
   if (use_mfma(a.G)) return launch_scan_mfma(a, B, stream);
-  // Groups of at most 4 q-heads (one chunk per kv-head): the split-range
-  // layout where split_range_groups says so.
-  if (const int z = split_range_groups(B, a.Hkv, num_splits)) {
+  // Groups of at most 4 q-heads (one chunk per kv-head, each wave serving the
+  // whole group): the split-range layout where split_range_groups says so.
+  // (Larger groups reach the VALU scan only in builds that move the
+  // matrix-core threshold, and take the shared layout's head chunks.)
+  const int z = a.G <= 4 ? split_range_groups(B, a.Hkv, num_splits) : 0;
+  if (z > 0) {
     const dim3 grid(a.Hkv, B, z);
     // One workgroup per pair whose waves stage all their splits: the
     // workgroup merges them itself (the single-launch mode's counters are
@@ -489,7 +492,8 @@ hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_
       case 1: return launch_split_range_g<1>(a, grid, merge, stream);
       case 2: return launch_split_range_g<2>(a, grid, merge, stream);
       case 3: return launch_split_range_g<3>(a, grid, merge, stream);
-      default: return launch_split_range_g<4>(a, grid, merge, stream);
+      case 4: return launch_split_range_g<4>(a, grid, merge, stream);
+      default: return hipErrorInvalidValue;
     }
   }
   switch (GH) {

@@ -24,7 +24,7 @@
 //          on its own MFMA: the effective weight P_hi + P_lo is within 2^-18
 //          relative of the fp32 one (a single bf16 part: 2^-9), which keeps the
 //          PV product as accurate as the reference's fp32 p * V
-//          (v2_splitkv.cu:200-204) to within fp32 summation noise. The fp32
+//          (v2_splitkv.cu:60-63) to within fp32 summation noise. The fp32
 //          sum l accumulates the same effective weights, so the weights stay
 //          normalised. The V tile goes through
 //          LDS: written row-major with a 16-byte-chunk XOR swizzle and read

@@ -89,3 +89,60 @@ def test_noalloc_rejects_oversize_and_accepts_empty(gpu):
     assert torch.equal(no_alloc(case, 64), with_workspace(case, 64))
     assert capi.balanced_launch_noalloc(*ptrs(case), out.data_ptr(), 0, Hq, Hkv, bs, mb, SCALE, 0,
                                         sp) == 0
+
+
+# Run in a fresh process, so that no call has resolved the device's scratch
+# array yet: the first call, made while the stream is captured into a graph,
+# is refused with hipErrorStreamCaptureUnsupported and launches nothing; after
+# one eager call, calls captured into a graph replay to the eager result.
+FIRST_CALL_UNDER_CAPTURE = r"""
+import math, sys
+import torch
+sys.path[:0] = {paths!r}
+import capi
+from cases import make_case
+case = make_case([700, 33, 2000], 32, 8, 16, pool_factor=1.25, seed=5, qkv_std=0.5)
+q, k, v, bt, sl = case
+B, Hq, Hkv, bs, mb = q.shape[0], q.shape[1], k.shape[2], k.shape[1], bt.shape[1]
+scale = 1.0 / math.sqrt(128)
+args = tuple(t.data_ptr() for t in case)
+out = torch.full_like(q, 3.0)
+s = torch.cuda.Stream()
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    rc_first = capi.balanced_launch_noalloc(*args, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, 64,
+                                            s.cuda_stream)
+torch.cuda.synchronize()
+assert rc_first == 900, rc_first
+assert (out.float() == 3.0).all(), "a refused call must launch nothing"
+eager = torch.empty_like(q)
+assert capi.balanced_launch_noalloc(*args, eager.data_ptr(), B, Hq, Hkv, bs, mb, scale, 64,
+                                    0) == 0
+torch.cuda.synchronize()
+g2 = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g2, stream=s):
+    rc = capi.balanced_launch_noalloc(*args, out.data_ptr(), B, Hq, Hkv, bs, mb, scale, 64,
+                                      s.cuda_stream)
+assert rc == 0, rc
+for _ in range(3):
+    out.fill_(0.0)
+    g2.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager), "replay differs from the eager call"
+print("FIRST_CALL_UNDER_CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture(gpu):
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    pkg = os.path.join(os.path.dirname(here), "mla-decode-kernels_amd")
+    paths = [os.path.join(pkg, "python"), os.path.join(pkg, "bench"), os.path.dirname(here)]
+    proc = subprocess.run([sys.executable, "-c", FIRST_CALL_UNDER_CAPTURE.format(paths=paths)],
+                          capture_output=True, text=True, timeout=240)
+    assert proc.returncode == 0 and "FIRST_CALL_UNDER_CAPTURE_OK" in proc.stdout, (
+        proc.stdout[-2000:] + proc.stderr[-3000:])
