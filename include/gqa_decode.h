@@ -81,7 +81,7 @@ GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cac
  * num_splits reaches 4 * max(1, CUs / (B * Hkv)) -- the waves the launch gives
  * each (request, kv-head) pair -- every split is scanned by one wave, each
  * wave walking a run of consecutive splits; with one workgroup per pair
- * (B * Hkv >= CUs) and at most 19 splits per wave (38 for 2-head groups, 76
+ * (B * Hkv >= CUs) and at most 19 splits per wave (37 for 2-head groups, 74
  * for 1-head groups, 25 for 3-head groups) that workgroup also merges its
  * splits, and no merge kernel runs. out is bitwise equal to
  * gqa_decode_v2_partial_launch followed by gqa_decode_v2_merge_launch in every

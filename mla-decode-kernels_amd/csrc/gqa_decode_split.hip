@@ -155,7 +155,14 @@ __global__ __launch_bounds__(64 * P) void gqa_decode_scan_kernel(const ScanArgs 
 // [slot][G][2], in floats), at most kStageBytes per workgroup (gfx950 has
 // 160 KiB of LDS per CU; the rest is left for the kernel's static LDS).
 constexpr int kStageBytes = 156 * 1024;
-inline int stage_cap(int G) { return kStageBytes / (kWavesPerHead * G * (kHeadDim + 2) * 4); }
+// Floats of one wave's stage of `slots` states, rounded up to 16 bytes so that
+// every wave's region (and its 16-byte acc stores) stays 16-byte aligned.
+__host__ __device__ constexpr int stage_wave_floats(int G, int slots) {
+  return (slots * G * (kHeadDim + 2) + 3) & ~3;
+}
+inline int stage_cap(int G) {
+  return kStageBytes / (kWavesPerHead * (G * (kHeadDim + 2) * 4 + 16));
+}
 inline int stage_slots(int G, int splits_per_wave) {
   return std::max(1, std::min(stage_cap(G), splits_per_wave));
 }
@@ -258,8 +265,8 @@ struct SplitStage {
 // scope); or, with one workgroup per pair whose stage holds every split, the
 // workgroup merges the staged states itself, split by split in index order
 // with the merge kernel's fold (kMerge: out equals partial + merge bit for
-// bit, with no second launch). Dynamic LDS: kWavesPerHead * slots * G * 130
-// floats.
+// bit, with no second launch). Dynamic LDS: kWavesPerHead regions of
+// stage_wave_floats(G, slots) floats.
 template <int G, bool kBlockUniform, RangeMode kMode>
 __global__ __launch_bounds__(64 * kWavesPerHead) void gqa_decode_split_range_kernel(
     const ScanArgs a, int slots) {
@@ -284,9 +291,9 @@ __global__ __launch_bounds__(64 * kWavesPerHead) void gqa_decode_split_range_ker
   const int rs = (int)min((int64_t)s_begin * chunk, (int64_t)S);
   const int re = (int)min((int64_t)s_end * chunk, (int64_t)S);
 
-  constexpr int kSlotFloats = G * (kHeadDim + 2);
+  const int wave_floats = stage_wave_floats(G, slots);
   float* const lds = reinterpret_cast<float*>(stage_lds);
-  float* wave_lds = lds + ph * slots * kSlotFloats;
+  float* wave_lds = lds + ph * wave_floats;
   SplitStage<G, kCoherent> stage{wave_lds, wave_lds + slots * G * kHeadDim, slots, 0, s_begin};
 
   uint4 qf[G];
@@ -338,13 +345,13 @@ __global__ __launch_bounds__(64 * kWavesPerHead) void gqa_decode_split_range_ker
       const int h = t >> 6, d2 = t & 63;
       float M = kNegInf;
       for (int w = 0; w < kWavesPerHead; ++w) {
-        const float* ml = lds + w * slots * kSlotFloats + slots * G * kHeadDim;
+        const float* ml = lds + w * wave_floats + slots * G * kHeadDim;
         const int n = (w + 1) * ns / kWavesPerHead - w * ns / kWavesPerHead;
         for (int j = 0; j < n; ++j) M = fmaxf(M, ml[(j * G + h) * 2]);
       }
       float L = 0.f, A0 = 0.f, A1 = 0.f;
       for (int w = 0; w < kWavesPerHead; ++w) {
-        const float* acc = lds + w * slots * kSlotFloats;
+        const float* acc = lds + w * wave_floats;
         const float* ml = acc + slots * G * kHeadDim;
         const int n = (w + 1) * ns / kWavesPerHead - w * ns / kWavesPerHead;
         for (int j = 0; j < n; ++j) {
@@ -413,7 +420,7 @@ template <int G, bool kBlockUniform>
 hipError_t launch_split_range(const ScanArgs& a, dim3 grid, bool merge, hipStream_t stream) {
   const int W = kWavesPerHead * (int)grid.z;
   const int slots = stage_slots(G, (a.num_splits + W - 1) / W);
-  const size_t lds = (size_t)kWavesPerHead * slots * G * (kHeadDim + 2) * sizeof(float);
+  const size_t lds = (size_t)kWavesPerHead * stage_wave_floats(G, slots) * sizeof(float);
   const dim3 block(64 * kWavesPerHead);
   if (merge)
     hipLaunchKernelGGL((gqa_decode_split_range_kernel<G, kBlockUniform, RangeMode::kMerge>), grid,

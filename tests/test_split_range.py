@@ -162,15 +162,18 @@ def test_fused_equals_two_launches(gpu, ns):
     assert torch.equal(out2, out)
 
 
-@pytest.mark.parametrize("G,ns", [(4, 4), (4, 7), (4, 37), (4, 76), (4, 77), (4, 100), (2, 150),
-                                  (1, 300)])
+@pytest.mark.parametrize("G,ns", [(4, 4), (4, 7), (4, 37), (4, 76), (4, 77), (4, 100), (3, 97),
+                                  (2, 150), (1, 290), (1, 300)])
 def test_v2_equals_partial_plus_merge(gpu, G, ns):
     """gqa_decode_v2_launch with one workgroup per pair merges the staged
     states inside the workgroup when every wave's splits fit its LDS stage
-    (4-head groups: up to 19 splits a wave, so up to 76 splits), and runs the
-    merge launch otherwise (the stage then also drains in mid-run): either way
-    its output equals the partial launch followed by the merge launch bit for
-    bit, and its workspace holds the partial launch's states."""
+    (4-head groups: up to 19 splits a wave, so up to 76 splits; 3-head groups
+    25, 2-head 37, 1-head 74), and runs the merge launch otherwise (the stage
+    then also drains in mid-run): either way its output equals the partial
+    launch followed by the merge launch bit for bit, and its workspace holds
+    the partial launch's states. (3, 97) and (1, 290) merge in the workgroup
+    with an odd number of staged floats per wave, whose LDS regions are padded
+    to 16 bytes."""
     Hkv = 2
     B = -(-cus() // Hkv)
     case = make_case(lengths(B, seed=ns, top=6000), G * Hkv, Hkv, 16, pool_factor=1.25, seed=G,
