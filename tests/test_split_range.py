@@ -17,6 +17,10 @@ device's CU count so that this layout is the one that runs. Checked:
   the same bits;
 - the single-launch form equal to partial + merge bit for bit, counters left
   at zero;
+- v2 with the in-workgroup merge equal to partial + merge bit for bit, on
+  both sides of the LDS stage's capacity (mid-run drains), up to the largest
+  split count (512);
+- replays of captured HIP graphs of each form equal to the eager launches;
 - bitwise repeatability.
 """
 
@@ -196,3 +200,80 @@ def test_v2_equals_partial_plus_merge(gpu, G, ns):
     assert torch.equal(ws1, ws2), f"G={G} ns={ns}: v2's workspace != the partial launch's"
     check_states(case, acc1, m1, l1, ns, [0, 1, 2, 3, 9, B - 1])
     assert_close(out, oracle(case, SCALE), 2e-2, 2e-2, f"v2 G={G} ns={ns}")
+
+
+@pytest.mark.parametrize("mode", ["merge_in_workgroup", "merge_launch", "fused"])
+def test_graph_replay(gpu, mode):
+    """The split-range launches captured in a HIP graph and replayed (new
+    queries written between replays, the eager launch in between): every
+    replay equals the eager launch bit for bit. merge_in_workgroup: one
+    workgroup per pair, v2 is one kernel; merge_launch: two workgroups per
+    pair, the partial kernel then the merge kernel; fused: the single-launch
+    entry point on a one-workgroup-per-pair batch. Nothing here records a
+    memset or allocates."""
+    Hq, Hkv = 8, 2
+    if mode == "merge_launch":
+        B, ns = cus() // (Hkv * 2), 16  # 2 workgroups per pair, 16 >= 4 * 2 splits
+        assert groups_per_pair(B, Hkv) == 2
+    else:
+        B, ns = -(-cus() // Hkv), 12
+        assert groups_per_pair(B, Hkv) == 1
+    case = make_case(lengths(B, seed=40), Hq, Hkv, 16, pool_factor=1.25, seed=41, poison=True)
+    q, k, v, bt, sl = case
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr())
+
+    def make_launch(out):
+        if mode == "fused":
+            ws, n = fused_workspace(B, Hq, ns, q.device)
+            return lambda: capi.v2_fused_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, 16, bt.shape[1],
+                                                SCALE, ns, ws.data_ptr(), n,
+                                                torch.cuda.current_stream().cuda_stream)
+        _, acc, m, l = alloc_ws(B, Hq, ns, q.device)
+        return lambda: capi.v2_launch(*ptrs, out.data_ptr(), B, Hq, Hkv, 16, bt.shape[1], SCALE,
+                                      ns, acc.data_ptr(), m.data_ptr(), l.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream)
+
+    out = torch.empty_like(q)
+    launch = make_launch(out)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert launch() == 0  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert launch() == 0
+    eager_out = torch.empty_like(q)
+    eager = make_launch(eager_out)
+    gen = torch.Generator(device="cpu").manual_seed(42)
+    for rep in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.device, torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert eager() == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out), f"{mode}: replay {rep} differs from the eager launch"
+    assert_close(out, oracle(case, SCALE), 2e-2, 2e-2, f"{mode}/graph")
+
+
+def test_largest_split_count(gpu):
+    """512 splits (GQA_DECODE_MAX_SPLITS) over one workgroup per pair: 128
+    splits per wave, so each wave's LDS stage (19 states for 4-head groups)
+    drains six times in mid-run, and the merge launch folds 512 states per
+    row in batches of 64. Against partial + merge (bitwise) and the oracle;
+    splits past the requests' ends hold the neutral state."""
+    Hq, Hkv, ns = 16, 4, 512
+    B = -(-cus() // Hkv)
+    case = make_case(lengths(B, seed=512, top=20000), Hq, Hkv, 16, pool_factor=1.25, seed=5,
+                     poison=True)
+    q, k, v, bt, sl = case
+    ws1, acc1, m1, l1 = partial(case, ns)
+    check_states(case, acc1, m1, l1, ns, [0, 1, 5, 11])
+    ref = torch.empty_like(q)
+    assert capi.v2_merge_launch(acc1.data_ptr(), m1.data_ptr(), l1.data_ptr(), ref.data_ptr(), B,
+                                Hq, ns, stream_ptr()) == 0
+    out = gqa_decode_v2(*case, SCALE, num_splits=ns)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert_close(out, oracle(case, SCALE), 2e-2, 2e-2, "ns512")
