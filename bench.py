@@ -528,7 +528,9 @@ def stream_probe(torch, cases, dev):
     dynamic one (256 persistent workgroups claiming items of 512 or 1024 token
     slots of one (request, kv-head)), with each workgroup's end time on the
     GPU's 100 MHz real-time counter (from the launch's first start, last of
-    the 20 timed launches): how much of a launch is its tail."""
+    the 20 timed launches): how much of a launch is its tail. Between the
+    two, grids of 64 and 128 workgroups: the ceiling of launches that leave
+    CUs idle."""
     import ctypes
 
     path = os.path.join(PKG_DIR, "lib", "libgqa_stream_probe.so")
@@ -544,7 +546,7 @@ def stream_probe(torch, cases, dev):
     v = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     k.random_(0, 256)
     v.random_(0, 256)
-    sink = torch.empty(requests * 8 * 256, dtype=torch.int32, device=dev)
+    sink = torch.empty(max(requests * 8 * 256, 128 * 1024), dtype=torch.int32, device=dev)
     sp = torch.cuda.current_stream().cuda_stream
     res = {}
     for pattern, pname, nsplit in ((0, "head_strided", 1), (1, "whole_slot", splits),
@@ -561,6 +563,26 @@ def stream_probe(torch, cases, dev):
                         "tbps": round(2 * nbytes / ms / 1e9, 3),
                         "frac_of_8tbps": round(2 * nbytes / ms / 1e9 / 8.0, 4)}
             log(f"stream probe {key}: {ms * 1e3:.2f} us, {2 * nbytes / ms / 1e9:.3f} TB/s")
+    # Grids that occupy only part of the CUs: what 64 or 128 CUs stream on
+    # their own (linear, 4 or 16 waves per workgroup), and config 3's gather
+    # at one split (8 requests x 32768 slots: grid (8 kv-heads, 8 requests),
+    # 64 workgroups of 4 waves) and at two (each request's halves as 16
+    # requests of 16384 slots: 128 workgroups) over the same bytes.
+    for pattern, pname, reqs, sl, nsplit in ((2, "linear_64wg_4w", requests, slots, 64),
+                                            (4, "linear_64wg_16w", requests, slots, 64),
+                                            (2, "linear_128wg_4w", requests, slots, 128),
+                                            (4, "linear_128wg_16w", requests, slots, 128),
+                                            (0, "head_strided_c3_1split", 8, 32768, 1),
+                                            (0, "head_strided_c3_2split", 16, 16384, 1)):
+        def launch():
+            rc = L.gqa_stream_probe_launch(k.data_ptr(), v.data_ptr(), sink.data_ptr(), pattern,
+                                           reqs, sl, nsplit, 1, sp)
+            if rc != 0:
+                raise RuntimeError(f"gqa_stream_probe_launch returned {rc}")
+        ms = cases.time_op(launch, warmup=3, runs=10)
+        res[pname] = {"median_us": round(ms * 1e3, 2), "tbps": round(2 * nbytes / ms / 1e9, 3),
+                      "frac_of_8tbps": round(2 * nbytes / ms / 1e9 / 8.0, 4)}
+        log(f"stream probe {pname}: {ms * 1e3:.2f} us, {2 * nbytes / ms / 1e9:.3f} TB/s")
     L.gqa_stream_probe_timed_launch.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [
         ctypes.c_void_p]
     L.gqa_stream_probe_timed_launch.restype = ctypes.c_int

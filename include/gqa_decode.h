@@ -64,7 +64,10 @@ GQA_DECODE_API int gqa_decode_v0_launch(const uint16_t* q, const uint16_t* k_cac
  * q-head group, 16-byte row loads, fp32 online-softmax state. Groups of 5-16
  * q-heads over 4 or 8 kv-heads run the matrix-core scan, one workgroup per
  * request with a wave per kv-head, when the batch alone fills the device
- * (B * Hkv * 4 >= 24 * CUs). Replaces gqa_decode_v1_launch
+ * (B * Hkv * 4 >= 24 * CUs). Groups of up to 4 q-heads run it too when the
+ * grid leaves CUs idle (B * Hkv < CUs) and max_blocks * block_size is at most
+ * 1024 tokens; such grids also give each workgroup up to 12 or 16 waves (8
+ * on the matrix-core scan). Replaces gqa_decode_v1_launch
  * (include/gqa_decode.h:12-16). */
 GQA_DECODE_API int gqa_decode_v1_launch(const uint16_t* q, const uint16_t* k_cache,
                          const uint16_t* v_cache, const int* block_table,

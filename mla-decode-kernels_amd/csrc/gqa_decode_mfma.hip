@@ -156,8 +156,15 @@ hipError_t launch_scan_mfma(const ScanArgs& args, int B, hipStream_t stream) {
     if (a.Hkv == 4) return launch_mfma_shape<4, true>(a, grid, stream);
     return launch_mfma_shape<8, true>(a, grid, stream);
   }
+  // Head-strided: 8 waves per split on grids that leave CUs idle (12 would
+  // spill: the kernel needs ~180 VGPRs, and 3 waves per SIMD leave 168).
   const dim3 grid(a.Hkv * a.nchunk, B, a.num_splits);
-  return launch_mfma_shape<kMWavesPerHead>(a, grid, stream);
+  switch (waves_per_split((int64_t)B * a.Hkv * a.nchunk, a.num_splits,
+                          (int64_t)a.max_blocks * a.block_size, kMWavesPerHead, 8,
+                          device_cu_count())) {
+    case 8: return launch_mfma_shape<8>(a, grid, stream);
+    default: return launch_mfma_shape<kMWavesPerHead>(a, grid, stream);
+  }
 }
 
 }  // namespace gqa

@@ -440,10 +440,27 @@ hipError_t launch_split_range_g(const ScanArgs& a, dim3 grid, bool merge, hipStr
                                    : launch_split_range<G, false>(a, grid, merge, stream);
 }
 
+// Waves per split of the shared layout: kWavesPerHead, or 8, 12 or 16 where
+// waves_per_split allows (max_p: 3 waves per SIMD for the 4-head scan's ~160
+// VGPRs, 4 for the smaller ones; more would spill inside the tile loop). With
+// few requests and splits (config 3 at 2 splits: 128 pairs x splits) the grid
+// occupies only part of the CUs, and a workgroup can only use its own CU: the
+// extra waves raise the rate at which each occupied CU streams its split.
+// Full grids keep kWavesPerHead.
 template <int GH>
 hipError_t launch_scan_gh(const ScanArgs& a, int B, hipStream_t stream) {
   const dim3 grid(a.Hkv * a.nchunk, B, a.num_splits);
-  return launch_scan_shape<GH, kWavesPerHead>(a, grid, stream);
+  constexpr int kMaxP = GH == 4 ? 12 : 16;
+  switch (waves_per_split((int64_t)B * a.Hkv * a.nchunk, a.num_splits,
+                          (int64_t)a.max_blocks * a.block_size, kWavesPerHead, kMaxP,
+                          device_cu_count())) {
+    case 16:
+      if constexpr (kMaxP >= 16) return launch_scan_shape<GH, 16>(a, grid, stream);
+      [[fallthrough]];
+    case 12: return launch_scan_shape<GH, 12>(a, grid, stream);
+    case 8: return launch_scan_shape<GH, 8>(a, grid, stream);
+    default: return launch_scan_shape<GH, kWavesPerHead>(a, grid, stream);
+  }
 }
 
 hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -478,7 +495,9 @@ hipError_t launch_scan(const uint16_t* q, const uint16_t* k_cache, const uint16_
   a.scale_log2e = (float)((double)scale * 1.4426950408889634);
   a.counters = counters;
   a.merge_out = counters ? merge_out : nullptr;  // the single-launch mode's output
-  if (use_mfma(a.G)) return launch_scan_mfma(a, B, stream);
+  if (use_mfma(a.G) || use_mfma_underfilled(B, a.Hkv, num_splits,
+                                             (int64_t)max_blocks * block_size, device_cu_count()))
+    return launch_scan_mfma(a, B, stream);
   // Groups of at most 4 q-heads (one chunk per kv-head, each wave serving the
   // whole group): the split-range layout where split_range_groups says so.
   // (Larger groups reach the VALU scan only in builds that move the

@@ -65,6 +65,44 @@ inline bool use_mfma_slot(int B, int Hkv, int G, int num_splits, int num_cus) {
          (int64_t)B * num_splits * Hkv * 4 >= (int64_t)24 * num_cus;
 }
 
+// Waves per split of a head-strided launch of `wgs` workgroups per split
+// index (requests x kv-heads x head chunks) over splits of a sequence of up
+// to s_max tokens: `base`, or the largest of 8, 12 and 16 (at most max_p)
+// that keeps the whole grid within one wave per SIMD of the device and gives
+// every wave at least two 16-token tiles of the longest split. Only a grid
+// that leaves CUs idle takes more than `base`: a workgroup streams through
+// its own CU alone, so more waves in it raise that CU's rate.
+inline int waves_per_split(int64_t wgs, int num_splits, int64_t s_max, int base, int max_p,
+                           int cus) {
+  const int64_t n = wgs * num_splits;
+  if (cus <= 0 || n <= 0 || num_splits <= 0) return base;
+  const int64_t chunk = ((s_max + num_splits - 1) / num_splits + 31) & ~int64_t(31);
+  const int64_t tiles = chunk / 16;
+  int P = base;
+  for (const int p : {8, 12, 16})
+    if (p <= max_p && n * p <= (int64_t)cus * 4 && tiles >= 2 * p) P = p;
+  return P;
+}
+
+// Groups of at most 4 q-heads take the matrix-core scan instead of the VALU
+// scan when the grid (one workgroup per request, kv-head and split) leaves
+// CUs idle and the splits are short (at most kShortSplit tokens): such a
+// launch is bound by each wave's chain of tiles, not by HBM, and the
+// matrix-core scan's chain is shorter. Measured on MI355X (32Q/8KV, B = 1..8)
+// against the VALU scan: 8-25 % faster at 64-512-token splits, 0-7 % at 1024,
+// 4-20 % slower at 2048-4096 and 11-36 % slower at 8192-32768, where the
+// VALU scan keeps more bytes in flight per CU. Full grids keep the VALU scan,
+// which streams ~5 % faster there.
+#ifndef GQA_MFMA_UNDERFILLED
+#define GQA_MFMA_UNDERFILLED 1
+#endif
+constexpr int64_t kShortSplit = 1024;
+inline bool use_mfma_underfilled(int B, int Hkv, int num_splits, int64_t s_max, int num_cus) {
+  if (!GQA_MFMA_UNDERFILLED || num_cus <= 0 || num_splits <= 0) return false;
+  const int64_t chunk = ((s_max + num_splits - 1) / num_splits + 31) & ~int64_t(31);
+  return (int64_t)B * Hkv * num_splits < num_cus && chunk <= kShortSplit;
+}
+
 // MFMA scan: QK^T and PV on v_mfma_f32_16x16x32_bf16, up to 16 q-heads of a
 // GQA group per wave. Launches one kernel: the slot-group layout over grid
 // (num_splits, B) where use_mfma_slot says so, else over grid

@@ -21,7 +21,9 @@
 //   linear        256 workgroups x 4 waves (one wave per SIMD) stream both
 //                 buffers front to back: wave g of W takes 4 KiB chunks g,
 //                 g + W, ... (4 K + 4 V loads of 1 KiB per chunk); the plain
-//                 sequential read, with no gather at all.
+//                 sequential read, with no gather at all. With fewer
+//                 workgroups (4 or 16 waves each) than CUs it measures what
+//                 the occupied CUs alone can stream.
 // Each lane folds what it loaded into one word written to `sink`, so no load
 // is dead.
 //
@@ -176,11 +178,11 @@ __global__ __launch_bounds__(256) void probe_whole_slot(const uint8_t* K, const 
   sink[((size_t)b * gridDim.x + blockIdx.x) * 256 + threadIdx.x] = acc;
 }
 
-template <bool kNT>
-__global__ __launch_bounds__(256) void probe_linear(const uint8_t* K, const uint8_t* V,
-                                                    uint32_t* sink, uint32_t bytes) {
+template <bool kNT, int W = 4>
+__global__ __launch_bounds__(64 * W) void probe_linear(const uint8_t* K, const uint8_t* V,
+                                                       uint32_t* sink, uint32_t bytes) {
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), waves = gridDim.x * 4;
+  const int wave = blockIdx.x * W + (threadIdx.x >> 6), waves = gridDim.x * W;
   const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, 0, bytes, 0x00020000);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, 0, bytes, 0x00020000);
   const int chunks = (int)(bytes / 4096u);
@@ -188,17 +190,18 @@ __global__ __launch_bounds__(256) void probe_linear(const uint8_t* K, const uint
   const uint32_t acc = stream_tiles<kNT>(rk, rv, mine, [&](int k, int i) {
     return (uint32_t)(wave + waves * k) * 4096u + (uint32_t)i * 1024u + 16u * lane;
   });
-  sink[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
+  sink[(size_t)blockIdx.x * 64 * W + threadIdx.x] = acc;
 }
 
 }  // namespace
 
 // Reads K and V ([requests, slots, 8 heads, 256 B] each) once in `pattern`
 // (0 head-strided, 1 whole-slot with `splits` workgroups per request, 2 linear
-// with `splits` workgroups in all) with non-temporal (nontemporal != 0) or
-// plain loads. sink holds one word per thread: requests * 8 * 256 words for
-// pattern 0, requests * splits * 256 for pattern 1, splits * 256 for pattern
-// 2. Requires slots % 64 == 0 (pattern 1: slots % (2 * splits) == 0), slots *
+// with `splits` workgroups in all, 4 linear with `splits` workgroups of 16
+// waves: with fewer workgroups than CUs, the most one CU streams) with
+// non-temporal (nontemporal != 0) or plain loads. sink holds one word per
+// thread: requests * 8 * 256 words for pattern 0, requests * splits * 256 for
+// pattern 1, splits * 256 for pattern 2, splits * 1024 for pattern 4. Requires slots % 64 == 0 (pattern 1: slots % (2 * splits) == 0), slots *
 // 2 KiB < 4 GiB (pattern 2: the whole buffer). Returns hipErrorInvalidValue for
 // other arguments, else the launch status.
 extern "C" __attribute__((visibility("default"))) int gqa_stream_probe_launch(
@@ -224,10 +227,16 @@ extern "C" __attribute__((visibility("default"))) int gqa_stream_probe_launch(
       hipLaunchKernelGGL(probe_whole_slot<true>, grid, dim3(256), 0, stream, K, V, sink, slots);
     else
       hipLaunchKernelGGL(probe_whole_slot<false>, grid, dim3(256), 0, stream, K, V, sink, slots);
-  } else if (pattern == 2) {
+  } else if (pattern == 2 || pattern == 4) {
     const uint64_t bytes = (uint64_t)requests * slots * kSlotBytes;
     if (splits < 1 || splits > 65535 || bytes >= (uint64_t(1) << 32)) return hipErrorInvalidValue;
-    if (nontemporal)
+    if (pattern == 4 && nontemporal)
+      hipLaunchKernelGGL((probe_linear<true, 16>), dim3(splits), dim3(1024), 0, stream, K, V, sink,
+                         (uint32_t)bytes);
+    else if (pattern == 4)
+      hipLaunchKernelGGL((probe_linear<false, 16>), dim3(splits), dim3(1024), 0, stream, K, V,
+                         sink, (uint32_t)bytes);
+    else if (nontemporal)
       hipLaunchKernelGGL(probe_linear<true>, dim3(splits), dim3(256), 0, stream, K, V, sink,
                          (uint32_t)bytes);
     else
