@@ -529,8 +529,9 @@ def stream_probe(torch, cases, dev):
     slots of one (request, kv-head)), with each workgroup's end time on the
     GPU's 100 MHz real-time counter (from the launch's first start, last of
     the 20 timed launches): how much of a launch is its tail. Between the
-    two, grids of 64 and 128 workgroups: the ceiling of launches that leave
-    CUs idle."""
+    two, grids of 64 and 128 workgroups (the ceiling of launches that leave
+    CUs idle) and the head-strided read through a block table of 16-slot
+    blocks, identity and shuffled (config 2's access pattern)."""
     import ctypes
 
     path = os.path.join(PKG_DIR, "lib", "libgqa_stream_probe.so")
@@ -558,6 +559,8 @@ def stream_probe(torch, cases, dev):
                 if rc != 0:
                     raise RuntimeError(f"gqa_stream_probe_launch returned {rc}")
             ms = cases.time_op(launch, warmup=5, runs=20)
+            if pattern == 0 and nt:
+                folds = sink[:requests * 8 * 256].clone()  # the paged reads' check below
             key = f"{pname}_{'nt' if nt else 'plain'}"
             res[key] = {"median_us": round(ms * 1e3, 2),
                         "tbps": round(2 * nbytes / ms / 1e9, 3),
@@ -580,6 +583,34 @@ def stream_probe(torch, cases, dev):
             if rc != 0:
                 raise RuntimeError(f"gqa_stream_probe_launch returned {rc}")
         ms = cases.time_op(launch, warmup=3, runs=10)
+        res[pname] = {"median_us": round(ms * 1e3, 2), "tbps": round(2 * nbytes / ms / 1e9, 3),
+                      "frac_of_8tbps": round(2 * nbytes / ms / 1e9 / 8.0, 4)}
+        log(f"stream probe {pname}: {ms * 1e3:.2f} us, {2 * nbytes / ms / 1e9:.3f} TB/s")
+    # The head-strided read through a block table of 16-slot blocks, as
+    # config 2's cache is read: an identity table (the pattern above, with the
+    # scalar block-id loads) and config 2's seeded shuffle of the pool.
+    L.gqa_stream_probe_paged_launch.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 2 + [
+        ctypes.c_void_p]
+    L.gqa_stream_probe_paged_launch.restype = ctypes.c_int
+    nblk = slots // 16
+    perm = torch.randperm(requests * nblk, generator=torch.Generator().manual_seed(0))
+    for pname, table in (("paged_identity", torch.arange(requests * nblk)), ("paged_shuffled", perm)):
+        bt = table.to(torch.int32).view(requests, nblk).to(dev)
+        def launch():
+            rc = L.gqa_stream_probe_paged_launch(k.data_ptr(), v.data_ptr(), bt.data_ptr(),
+                                                 sink.data_ptr(), requests, nblk, sp)
+            if rc != 0:
+                raise RuntimeError(f"gqa_stream_probe_paged_launch returned {rc}")
+        ms = cases.time_op(launch, warmup=5, runs=20)
+        # Every lane sums its loads' folds: through the identity table each
+        # lane reads what it reads in the head-strided pattern, and through
+        # the shuffled one the lanes' sum over the grid is the same sum, if
+        # every 16 bytes of both pools are read exactly once.
+        got = sink[:requests * 8 * 256]
+        if pname == "paged_identity" and not torch.equal(got, folds):
+            raise RuntimeError("paged probe (identity table) read other bytes than head-strided")
+        if (int(got.to(torch.int64).sum()) - int(folds.to(torch.int64).sum())) % 2**32:
+            raise RuntimeError(f"{pname}: the pools were not read exactly once")
         res[pname] = {"median_us": round(ms * 1e3, 2), "tbps": round(2 * nbytes / ms / 1e9, 3),
                       "frac_of_8tbps": round(2 * nbytes / ms / 1e9 / 8.0, 4)}
         log(f"stream probe {pname}: {ms * 1e3:.2f} us, {2 * nbytes / ms / 1e9:.3f} TB/s")

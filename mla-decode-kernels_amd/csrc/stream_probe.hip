@@ -24,8 +24,15 @@
 //                 sequential read, with no gather at all. With fewer
 //                 workgroups (4 or 16 waves each) than CUs it measures what
 //                 the occupied CUs alone can stream.
+//   paged         the head-strided pattern through a block table: 16-slot
+//                 blocks (32 KiB) at the ids the table gives, as config 2's
+//                 cache is read (gqa_stream_probe_paged_launch).
 // Each lane folds what it loaded into one word written to `sink`, so no load
-// is dead.
+// is dead. Every pattern takes its wave index through readfirstlane, as the
+// decode kernels do: derived from threadIdx alone, the index is not known to
+// be wave-uniform, the tile loop's branches then run under exec masks, and
+// their conservative load waits slowed the paged read from 157 to 181 us
+// (identity table).
 //
 // The timed entry point (gqa_stream_probe_timed_launch) also records, per
 // workgroup, the 100 MHz real-time counter at its start and end, which shows
@@ -104,7 +111,7 @@ __global__ __launch_bounds__(256) void probe_head_strided(const uint8_t* K, cons
                                                           unsigned long long* times) {
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
   const int h = blockIdx.x ^ 1, b = blockIdx.y;
-  const int lane = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane >> 4, c = lane & 15;
   const size_t base = (size_t)b * slots * kSlotBytes;
   const uint32_t bytes = (uint32_t)slots * kSlotBytes;
@@ -126,7 +133,7 @@ __global__ __launch_bounds__(256) void probe_dynamic(const uint8_t* K, const uin
                                                      unsigned long long* times) {
   __shared__ int next_item[2];
   const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-  const int lane = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane >> 4, c = lane & 15;
   const int per_chunk = requests * kHeads, nitems = per_chunk * (slots / chunk);
   uint32_t acc = 0;
@@ -166,7 +173,7 @@ template <bool kNT>
 __global__ __launch_bounds__(256) void probe_whole_slot(const uint8_t* K, const uint8_t* V,
                                                         uint32_t* sink, int slots) {
   const int sp = blockIdx.x, b = blockIdx.y;
-  const int lane = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int per = slots / gridDim.x;
   const size_t base = ((size_t)b * slots + (size_t)sp * per) * kSlotBytes;
   const uint32_t bytes = (uint32_t)per * kSlotBytes;
@@ -182,7 +189,8 @@ template <bool kNT, int W = 4>
 __global__ __launch_bounds__(64 * W) void probe_linear(const uint8_t* K, const uint8_t* V,
                                                        uint32_t* sink, uint32_t bytes) {
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * W + (threadIdx.x >> 6), waves = gridDim.x * W;
+  const int wave = blockIdx.x * W + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = gridDim.x * W;
   const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, 0, bytes, 0x00020000);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, 0, bytes, 0x00020000);
   const int chunks = (int)(bytes / 4096u);
@@ -193,7 +201,65 @@ __global__ __launch_bounds__(64 * W) void probe_linear(const uint8_t* K, const u
   sink[(size_t)blockIdx.x * 64 * W + threadIdx.x] = acc;
 }
 
+// Paged head-strided: the head-strided pattern over a paged cache. K and V
+// are pools of 16-slot blocks (32 KiB each, slots of 8 kv-heads x 256 B);
+// request b's tile k (16 tokens) is block bt[b * nblk + k], its id read as a
+// scalar through the constant address space, as the VALU scan reads it from
+// its block table. With a shuffled table this is config 2's access pattern
+// (block size 16) without the scan's arithmetic.
+__global__ __launch_bounds__(256) void probe_paged(const uint8_t* K, const uint8_t* V,
+                                                   const int* bt, uint32_t* sink, int nblk) {
+  const int h = blockIdx.x ^ 1, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, ph = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 4, c = lane & 15;
+  const auto* btc = (const __attribute__((address_space(4))) int*)(bt + (size_t)b * nblk);
+  const int my = round_robin_count(nblk, ph);
+  const uint32_t bytes = 16 * kSlotBytes - (uint32_t)h * kRowBytes;
+  uint32_t acc = 0;
+  uint4 t[2][8];
+  auto issue = [&](int k, uint4 (&d)[8]) {
+    const size_t base = (size_t)btc[ph + 4 * k] * (16 * kSlotBytes) + (size_t)h * kRowBytes;
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(K + base), 0, bytes, 0x00020000);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)(V + base), 0, bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t off = (uint32_t)(4 * i + r) * kSlotBytes + 16 * c;
+      d[i] = load16<true>(rk, off);
+      d[4 + i] = load16<true>(rv, off);
+    }
+  };
+  if (my > 0) issue(0, t[0]);
+  for (int k = 0; k < my; k += 2) {
+    if (k + 1 < my) issue(k + 1, t[1]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += fold(t[0][i]);
+    if (k + 1 >= my) break;
+    if (k + 2 < my) issue(k + 2, t[0]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += fold(t[1][i]);
+  }
+  sink[((size_t)b * gridDim.x + blockIdx.x) * 256 + threadIdx.x] = acc;
+}
+
 }  // namespace
+
+// Paged head-strided read (non-temporal loads): K and V are pools of
+// requests * nblk blocks of 16 slots (32 KiB each), bt an int32 table
+// [requests, nblk] of block ids in [0, requests * nblk); grid (8 kv-heads,
+// requests) x 4 waves. sink holds requests * 8 * 256 words. Returns
+// hipErrorInvalidValue for a null pointer, requests outside [1, 65535] or
+// nblk < 1, else the launch status. The ids are not checked: every one must
+// lie in the pool.
+extern "C" __attribute__((visibility("default"))) int gqa_stream_probe_paged_launch(
+    const void* k, const void* v, const int* bt, uint32_t* sink, int requests, int nblk,
+    hipStream_t stream) {
+  if (!k || !v || !bt || !sink || requests < 1 || requests > 65535 || nblk < 1)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(probe_paged, dim3(kHeads, requests), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), bt, sink,
+                     nblk);
+  return hipGetLastError();
+}
 
 // Reads K and V ([requests, slots, 8 heads, 256 B] each) once in `pattern`
 // (0 head-strided, 1 whole-slot with `splits` workgroups per request, 2 linear

@@ -218,7 +218,8 @@ def test_stream_probe_patterns(gpu, capsys):
     # bench.py --stream-probe: every pattern reads config 2's 1 GiB of K and V
     # at a physical rate; the timed patterns record every workgroup's end (in
     # order: first <= median <= last, the last within the launch); the dynamic
-    # pattern leaves its claim counters at zero (stream_probe checks that).
+    # pattern leaves its claim counters at zero, and the paged reads cover
+    # both pools exactly once (stream_probe checks both).
     import torch
 
     import bench
@@ -228,7 +229,9 @@ def test_stream_probe_patterns(gpu, capsys):
     line = [ln for ln in capsys.readouterr().out.splitlines() if ln.startswith('{"stream_probe"')]
     res = json.loads(line[-1])["results"]
     for key in ("head_strided_nt", "head_strided_plain", "whole_slot_nt", "linear_nt",
-                "timed_head_strided", "dynamic_512", "dynamic_1024"):
+                "linear_64wg_4w", "linear_64wg_16w", "linear_128wg_4w", "linear_128wg_16w",
+                "head_strided_c3_1split", "head_strided_c3_2split", "paged_identity",
+                "paged_shuffled", "timed_head_strided", "dynamic_512", "dynamic_1024"):
         assert 1.0 < res[key]["tbps"] < 8.0, (key, res[key])
     for key in ("timed_head_strided", "dynamic_512", "dynamic_1024"):
         e = res[key]["wg_end_us"]
