@@ -47,8 +47,8 @@ sys.path.insert(0, os.path.join(os.path.dirname(_HERE), "python"))
 
 import cases  # noqa: E402
 import provenance  # noqa: E402
-from binding import (KERNELS, gqa_decode_balanced, gqa_decode_v2,  # noqa: E402
-                     num_splits_heuristic, prefer_balanced)
+from binding import (KERNELS, automatic_choice, gqa_decode_balanced,  # noqa: E402
+                     gqa_decode_v2)
 
 KERNEL_LIB = os.path.join(os.path.dirname(_HERE), "lib", "libgqa_decode_hip.so")
 
@@ -111,8 +111,7 @@ def run_cell(Hq, Hkv, S, B, bs, baseline, num_cus, warmup=None, runs=None):
     warmup = dw if warmup is None else warmup
     runs = dr if runs is None else runs
     mb = case[3].shape[1]
-    choice = ("balanced" if prefer_balanced(B, Hq, Hkv, bs, mb, num_cus)
-              else num_splits_heuristic(B, Hq, Hkv, bs, mb, num_cus))
+    choice = automatic_choice(B, Hq, Hkv, bs, mb, num_cus) or "balanced"
     checks["v2_auto"] = cases.spot_check(
         lambda *a: gqa_decode_v2(*a, num_splits=0), case, scale, label="v2 automatic")
     with_balanced = Hq // Hkv <= 16  # the balanced launcher's groups (Hkv = 8 here)

@@ -41,6 +41,9 @@ num_splits_heuristic = _ext.num_splits_heuristic
 # v2 op's num_splits=0 uses to choose it.
 gqa_decode_balanced = _ext.gqa_decode_balanced
 prefer_balanced = _ext.prefer_balanced
+# What gqa_decode_v2(..., num_splits=0) runs: 0 = the balanced launch, else the
+# split count.
+automatic_choice = _ext.automatic_choice
 
 # "v2" runs with its default num_splits=8; pass num_splits explicitly via
 # gqa_decode_v2 to override (0 = heuristic).

@@ -10,8 +10,9 @@
 // into the three arrays instead of three, and none at all for one split (the
 // single-pass kernel runs instead, with bitwise the same output). With
 // num_splits == 0 the op runs the token-balanced launch where
-// gqa_decode_prefer_balanced says so, else the split heuristic's count; the
-// balanced launch is also its own op (gqa_decode_balanced).
+// gqa_decode_prefer_balanced says so, else the split heuristic's count (one
+// split for sequences of at most 512 tokens; automatic_choice); the balanced
+// launch is also its own op (gqa_decode_balanced).
 //
 // This file is host-only C++ (compiled by g++); all device code lives in the
 // hipcc-built libgqa_decode_hip.so it links against.
@@ -149,6 +150,27 @@ torch::Tensor run_balanced(const GqaDims& d, const torch::Tensor& q, const torch
   return out;
 }
 
+// The v2 op's choice for num_splits == 0 (B > 0): 0 for the token-balanced
+// launch, where the split launch's per-request splits would be uneven
+// (gqa_decode_prefer_balanced), else a split count: one for sequences of at
+// most 512 tokens, the heuristic's otherwise. Through this op a split launch
+// also allocates its workspace and launches the merge, a few us that splits
+// of such short sequences do not win back. Measured on MI355X through this
+// op, S = 512, block 16: B = 1 one split 11.1 us (32Q/8KV) and 12.2 us
+// (64Q/8KV) against 13.3 and 13.4 at the heuristic's 4; B = 8 14.1 and 13.8
+// (v1) against 14.6 and 14.4. Through the C ABI, with the workspace
+// allocated once, the 4 splits win (config 1: 7.7 us against 8.8), so the
+// heuristic itself keeps them.
+int64_t automatic_choice(int64_t B, int64_t Hq, int64_t Hkv, int64_t block_size,
+                         int64_t max_blocks, int64_t num_cus) {
+  if (gqa_decode_prefer_balanced((int)B, (int)Hq, (int)Hkv, (int)block_size, (int)max_blocks,
+                                 (int)num_cus))
+    return 0;
+  if (max_blocks * block_size <= 512) return 1;
+  return gqa_decode_pick_num_splits((int)B, (int)Hq, (int)Hkv, (int)block_size, (int)max_blocks,
+                                    (int)num_cus);
+}
+
 torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
                             torch::Tensor block_table, torch::Tensor seq_lens, double scale,
                             int64_t num_splits) {
@@ -157,14 +179,9 @@ torch::Tensor gqa_decode_v2(torch::Tensor q, torch::Tensor k_cache, torch::Tenso
               "num_splits must be in [1, 512] (or 0 for the heuristic)");
   const c10::DeviceGuard guard(q.device());
   if (num_splits == 0 && d.B > 0) {
-    // Automatic choice: the token-balanced launch where the split launch's
-    // per-request splits would be uneven, else the split heuristic's count.
-    const int cus = device_cus(q);
-    if (gqa_decode_prefer_balanced((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
-                                   (int)d.max_blocks, cus))
+    num_splits = automatic_choice(d.B, d.Hq, d.Hkv, d.block_size, d.max_blocks, device_cus(q));
+    if (num_splits == 0)
       return run_balanced(d, q, k_cache, v_cache, block_table, seq_lens, scale, 0);
-    num_splits = gqa_decode_pick_num_splits((int)d.B, (int)d.Hq, (int)d.Hkv, (int)d.block_size,
-                                            (int)d.max_blocks, cus);
   }
   if (num_splits == 0) num_splits = 1;  // empty batch
   TORCH_CHECK(num_splits >= 1, "num_splits heuristic failed");
@@ -231,6 +248,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "gqa_decode_prefer_balanced(B, Hq, Hkv, block_size, max_blocks, num_cus)", py::arg("B"),
         py::arg("Hq"), py::arg("Hkv"), py::arg("block_size"), py::arg("max_blocks"),
         py::arg("num_cus") = 0);
+  m.def("automatic_choice", &automatic_choice,
+        "gqa_decode_v2's choice for num_splits=0 (B > 0): 0 = the token-balanced launch, "
+        "else the split count",
+        py::arg("B"), py::arg("Hq"), py::arg("Hkv"), py::arg("block_size"),
+        py::arg("max_blocks"), py::arg("num_cus") = 0);
   m.def("num_splits_heuristic", &gqa_decode_num_splits,
         "gqa_decode_pick_num_splits(B, Hq, Hkv, block_size, max_blocks, num_cus)",
         py::arg("B"), py::arg("Hq"), py::arg("Hkv"), py::arg("block_size"),

@@ -371,6 +371,23 @@ def test_binding_exports(binding):
         capi.pick_num_splits(32, 32, 8, 16, 512, 256)
 
 
+@pytest.mark.parametrize("B,Hq,bs,mb", [(1, 32, 16, 32), (8, 64, 64, 8), (1, 32, 16, 33),
+                                        (8, 32, 64, 512), (128, 32, 16, 512), (32, 64, 64, 512),
+                                        (2, 32, 1, 512), (2, 32, 1, 513)])
+def test_op_automatic_choice(binding, B, Hq, bs, mb):
+    # gqa_decode_v2(num_splits=0): the balanced launch (0) where
+    # gqa_decode_prefer_balanced says so, else one split for block tables of
+    # at most 512 tokens, else the C ABI heuristic's count.
+    cus = 256
+    if capi.prefer_balanced(B, Hq, 8, bs, mb, cus):
+        want = 0
+    elif mb * bs <= 512:
+        want = 1
+    else:
+        want = capi.pick_num_splits(B, Hq, 8, bs, mb, cus)
+    assert binding.automatic_choice(B, Hq, 8, bs, mb, cus) == want
+
+
 @pytest.mark.parametrize("kernel", ["v0", "v1", "v2"])
 def test_op_rejects_host_tensors(binding, kernel):
     with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):

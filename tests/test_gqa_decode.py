@@ -311,6 +311,23 @@ def test_heuristic_num_splits(gpu):
     run_and_check(lambda *a: gqa_decode_v2(*a, num_splits=0), case)
 
 
+@pytest.mark.parametrize("max_blocks", [32, 33])
+def test_op_automatic_choice_short_sequences(gpu, max_blocks):
+    # The op's automatic choice takes one split for block tables of at most
+    # 512 tokens (output bitwise v1's), where the C ABI's heuristic gives 4
+    # (config 1's shape); one more block and the heuristic's count runs.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    S = [500, 512] if max_blocks == 32 else [500, 528]
+    case = make_case(S, 32, 8, 16, pool_factor=1.25, seed=max_blocks, max_blocks=max_blocks)
+    ns = capi.pick_num_splits(2, 32, 8, 16, max_blocks, cus)
+    assert ns > 1
+    out = gqa_decode_v2(*case, SCALE, num_splits=0)
+    want = gqa_decode_v1(*case, SCALE) if max_blocks == 32 else \
+        gqa_decode_v2(*case, SCALE, num_splits=ns)
+    assert torch.equal(out, want)
+    assert_close(out, oracle(case, SCALE), 2e-2, 2e-2, f"auto, max_blocks={max_blocks}")
+
+
 def test_op_input_errors_on_device(gpu):
     q, k, v, bt, sl = ref_case(CASES["a_base"])
     with pytest.raises(RuntimeError, match="Hq must be divisible by Hkv"):
