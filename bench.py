@@ -666,8 +666,10 @@ def host_cpu_record(threads, source):
 
 def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
     """The MLA oracle (oracle/mla_decode_oracle.c) on this host's cores over
-    whole requests of the workload (~10 s), scaled to one full step; its output
-    on the sample is compared with the GPU's (out within 2e-2, lse 5e-3)."""
+    whole requests of the workload (~10 s per run), run until ~10 s of CPU
+    time has been timed (at least 3 runs), the median run scaled to one full
+    step; its output on the sample is compared with the GPU's (out within
+    2e-2, lse 5e-3)."""
     import numpy as np
 
     from cases import mla_host_case
@@ -688,12 +690,12 @@ def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
         tokens += S_list[b]
     hc = mla_host_case(case, sample)
     times = []
-    for _ in range(3):
+    while len(times) < 3 or (sum(times) < budget_s and len(times) < 1000):
         t0 = time.perf_counter()
         ref_out, ref_lse = c_oracle.mla_decode_ref(*hc, scale, causal=args.causal,
                                                    nthreads=threads)
         times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
+    t = sorted(times)[len(times) // 2]
     frac = tokens / sum(S_list)
     cpu_us = t / frac * 1e6
     got = out[sample].float().cpu().numpy()
@@ -709,15 +711,17 @@ def cpu_baseline_mla(args, case, out, lse, S_list, scale, gpu_us):
     return {"value": round(cpu_us, 1), "unit": "us", **host_cpu_record(threads, source),
             "kind": "port",
             "sample": f"requests {sample[0]}..{sample[-1]} ({len(sample)} of {B}, "
-                      f"{tokens} tokens = {frac * 100:.1f}% of the step), median of 3 runs of "
-                      f"oracle/mla_decode_oracle.c, scaled to the full step",
+                      f"{tokens} tokens = {frac * 100:.1f}% of the step), median of "
+                      f"{len(times)} runs ({sum(times):.1f} s) of oracle/mla_decode_oracle.c, "
+                      f"scaled to the full step",
             "speedup_gpu_vs_cpu": round(cpu_us / gpu_us, 1),
             "spot_check_max_abs": err, "spot_check_lse_max_abs": lse_err}
 
 
 def cpu_baseline(args, case, out, S_list, scale, gpu_us):
     """The oracle on this host's cores over a bounded sample of the workload
-    (whole requests, at most ~10 s per run), scaled to one full step."""
+    (whole requests, at most ~10 s per run), run until ~10 s of CPU time has
+    been timed (at least 3 runs), the median run scaled to one full step."""
     import numpy as np
 
     from cases import host_case
@@ -741,11 +745,11 @@ def cpu_baseline(args, case, out, S_list, scale, gpu_us):
         tokens += S_list[b]
     hc = host_case(case, sample)
     times = []
-    for _ in range(3):
+    while len(times) < 3 or (sum(times) < budget_s and len(times) < 1000):
         t0 = time.perf_counter()
         ref_out = c_oracle.attention_ref(*hc, scale, nthreads=threads)
         times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
+    t = sorted(times)[len(times) // 2]
     frac = tokens / sum(S_list)
     cpu_us = t / frac * 1e6
     got = out[sample].float().cpu().numpy()
@@ -759,8 +763,9 @@ def cpu_baseline(args, case, out, S_list, scale, gpu_us):
     return {"value": round(cpu_us, 1), "unit": "us", **host_cpu_record(threads, source),
             "kind": "port",
             "sample": f"requests {sample[0]}..{sample[-1]} ({len(sample)} of {B}, "
-                      f"{tokens} tokens = {frac * 100:.1f}% of the step), median of 3 runs of "
-                      f"oracle/gqa_decode_oracle.c, scaled to the full step",
+                      f"{tokens} tokens = {frac * 100:.1f}% of the step), median of "
+                      f"{len(times)} runs ({sum(times):.1f} s) of oracle/gqa_decode_oracle.c, "
+                      f"scaled to the full step",
             "speedup_gpu_vs_cpu": round(cpu_us / gpu_us, 1),
             "spot_check_max_abs": err}
 
