@@ -10,8 +10,11 @@ lengths, causal and not, zero-length requests; inputs N(0,1) bf16 with NaN in
 every cache slot a request must not read. Added: split counts 1..8 and the
 automatic one, block sizes off the 32-token tile (the per-lane gather),
 query-row counts that are not multiples of 32 or exceed one 128-row group,
-bitwise repeatability, the FlashMLA-style Python surface, and a full-size
-benchmark batch checked on a subset of requests. Tolerance: out within
+bitwise repeatability, the FlashMLA-style Python surface, a full-size
+benchmark batch checked on a subset of requests, and exact properties of
+whole benchmark batches with no oracle in the loop (twice the cache with half
+the scale: twice out and the same lse, bit for bit; every output between its
+value rows' extremes). Tolerance: out within
 atol = rtol = 2e-2 of the fp32 oracle (softmax weights are rounded to bf16
 for the PV product, as in the GQA matrix-core scan), lse within 5e-3.
 """
@@ -533,3 +536,59 @@ def test_balanced_overflowing_late_key(gpu):
         got = run_balanced(case, False, nwg)
         assert torch.isfinite(got[0].float()).all()
         check(got, want, f"bal overflow/n{nwg}")
+
+
+def benchmark_case(name="mla_4k"):
+    cfg = MLA_CONFIGS[name]
+    S_list = mla_seq_lens(cfg["B"], cfg["S_mean"], seed=0, s_q=cfg["s_q"])
+    return make_mla_case(S_list, cfg["s_q"], cfg["h_q"], cfg["bs"], pool_factor=1.1, seed=0,
+                         device="cuda")
+
+
+def launchers(case):
+    ns = capi.mla_pick_num_splits(case[0].shape[0], case[0].shape[1], case[0].shape[2],
+                                  case[1].shape[1], case[2].shape[1], 0)
+    return {"split": lambda c, causal, s: run(c, causal, ns, s),
+            "balanced": lambda c, causal, s: run_balanced(c, causal, 256, s)}
+
+
+@pytest.mark.parametrize("name,causal", [("mla_4k", False), ("mla_4k_sq2", True)])
+def test_cache_scale_property(gpu, name, causal):
+    # A latent row is the key (576 dims) and the value (its first 512): twice
+    # the cache with half the scale gives the same scores bit for bit (binary
+    # floating point scales by 2 without rounding), so twice out and the same
+    # lse, bit for bit, at the benchmark batch's full size, no oracle needed.
+    case = benchmark_case(name)
+    q, kv, bt, sl = case
+    doubled = (q, kv * 2, bt, sl)
+    for label, f in launchers(case).items():
+        print(f"{name} cache scale {label}", flush=True)
+        out, lse = f(case, causal, SCALE)
+        out2, lse2 = f(doubled, causal, SCALE / 2)
+        assert torch.equal(out2, out * 2), f"{name}/{label}: out(2C, scale/2) != 2 out(C, scale)"
+        assert torch.equal(lse2, lse), f"{name}/{label}: lse changed"
+
+
+def test_convex_combination(gpu):
+    # out[b, i, h] is a convex combination of the request's value rows (the
+    # first 512 dims of its latent rows): every element lies between their
+    # smallest and largest value in that dimension (up to out's bf16 rounding).
+    case = benchmark_case("mla_4k")
+    q, kv, bt, sl = case
+    bs = kv.shape[1]
+    lo, hi = [], []
+    for b, S in enumerate(sl.tolist()):
+        nblk = -(-S // bs)
+        rows = kv[bt[b, :nblk].long()].reshape(nblk * bs, 576)[:S, :512].float()
+        lo.append(rows.amin(0))
+        hi.append(rows.amax(0))
+    lo = torch.stack(lo)[:, None, None]
+    hi = torch.stack(hi)[:, None, None]
+    slack = torch.maximum(lo.abs(), hi.abs()) * 2.0 ** -7 + 1e-6
+    for label, f in launchers(case).items():
+        print(f"mla_4k convex combination {label}", flush=True)
+        out = f(case, False, SCALE)[0].float()
+        assert torch.isfinite(out).all()
+        below = (out < lo - slack).sum().item()
+        above = (out > hi + slack).sum().item()
+        assert below == 0 and above == 0, f"{label}: {below} below, {above} above"
