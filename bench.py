@@ -107,17 +107,30 @@ def read_traffic(config, kernel, num_splits):
     return None
 
 
-def kernel_name(kernel, group, balanced=False, hkv=8):
-    """The dominant kernel of one step: v0's kernel, else the token-balanced or
-    split-rule scan the dispatcher picks: split launches use the matrix cores
-    from 5 q-heads per group, the balanced launcher whenever there are 4 or 8
-    kv-heads."""
+def kernel_name(kernel, group, balanced=False, hkv=8, B=1, num_splits=1, s_max=0, cus=0):
+    """The dominant kernel of one step, by the launchers' rules
+    (csrc/gqa_scan.hpp, csrc/gqa_decode_split.hip): v0's kernel; the
+    token-balanced scan (matrix-core over 4 or 8 kv-heads); for split launches
+    the matrix-core scan from 5 q-heads per group, and for smaller groups the
+    split-range kernel once the split count reaches 4 waves' worth per
+    (request, kv-head) of one round of one workgroup per CU, the matrix-core
+    scan on grids of fewer workgroups than CUs whose splits are at most 1024
+    tokens, else the VALU scan."""
     if kernel == "v0":
         return "gqa_decode_v0_kernel"
     if balanced:
         return ("gqa_decode_balanced_mfma_kernel" if hkv in (4, 8)
                 else "gqa_decode_balanced_kernel")
-    return "gqa_decode_mfma_kernel" if group >= 5 else "gqa_decode_scan_kernel"
+    if group >= 5:
+        return "gqa_decode_mfma_kernel"
+    pairs = B * hkv
+    ns = num_splits if kernel == "v2" else 1
+    chunk = (-(-s_max // ns) + 31) // 32 * 32
+    if cus > 0 and pairs * ns < cus and chunk <= 1024:
+        return "gqa_decode_mfma_kernel"
+    if ns >= 2 and cus > 0 and ns >= 4 * (cus // pairs if cus > pairs else 1):
+        return "gqa_decode_split_range_kernel"
+    return "gqa_decode_scan_kernel"
 
 
 def provenance_stamp(kind, lib_path):
@@ -222,9 +235,12 @@ def main(argv=None):
 
     ns = args.num_splits
     cus = props.multi_processor_count
-    # v2 with num_splits 0 makes the torch op's automatic choice: the
+    # v2 with num_splits 0 takes the C ABI's automatic rule: the
     # token-balanced launch where gqa_decode_prefer_balanced says so, else the
-    # split heuristic's count.
+    # split heuristic's count. (The torch op also takes one split for block
+    # tables of at most 512 tokens, where it allocates the split workspace
+    # inside the call; here the workspace is allocated once, as a C ABI
+    # caller would, and the heuristic's count is the faster one.)
     balanced = args.kernel == "balanced" or (
         args.kernel == "v2" and ns == 0 and capi.prefer_balanced(B, Hq, Hkv, bs, mb, cus) == 1)
     if args.kernel == "v2" and ns == 0 and not balanced:
@@ -361,7 +377,10 @@ def main(argv=None):
         "kv_bytes": kvb,
         "sol_us": round(sol, 3),
         "op_median_us": round(op_ms * 1e3, 3) if op_ms is not None else None,
-        "roofline": {"bound": "hbm", "kernel": kernel_name(args.kernel, Hq // Hkv, balanced, Hkv),
+        "roofline": {"bound": "hbm",
+                     "kernel": kernel_name(args.kernel, Hq // Hkv, balanced, Hkv, B,
+                                           ns if not balanced else 1, mb * bs,
+                                           props.multi_processor_count),
                      "achieved": round(achieved, 1),
                      "peak": 8000.0, "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
                      "avg_kernel_us": round(kern_avg_us, 3),

@@ -1,7 +1,9 @@
 // Single-pass / split-KV partial scan on the gfx950 matrix cores, used for
 // GQA groups of 5 or more q-heads (16 per MFMA column block, larger groups in
-// chunks of 16): the per-tile work is the MFMA scan of gqa_scan_mfma.hpp;
-// this file holds the split-rule kernel and its launches.
+// chunks of 16), and for smaller groups on grids that leave CUs idle with
+// splits of at most 1024 tokens (use_mfma_underfilled in gqa_scan.hpp): the
+// per-tile work is the MFMA scan of gqa_scan_mfma.hpp; this file holds the
+// split-rule kernel and its launches.
 //
 // Same split rule, workspace contract and fixed-order merges as the VALU scan
 // in gqa_decode_split.hip, including the single-launch mode.
@@ -17,9 +19,10 @@ namespace {
 
 constexpr int kMWavesPerHead = 4;
 
-// Two launch layouts. Head-strided (kSlot = false): a workgroup of P waves per
-// (kv-head, q-head chunk, request, split), the waves dealing the segment's
-// tiles round-robin and merging through LDS. Slot-group (kSlot = true): one
+// Two launch layouts. Head-strided (kSlot = false): a workgroup of P waves (4,
+// or 8 on grids that leave CUs idle) per (kv-head, q-head chunk, request,
+// split), the waves dealing the segment's tiles round-robin and merging
+// through LDS. Slot-group (kSlot = true): one
 // workgroup per (split, request) with one wave per kv-head (P = Hkv, groups of
 // at most 16 q-heads), every wave walking every tile of the segment for its
 // own head and writing its state directly. In the slot-group layout the waves

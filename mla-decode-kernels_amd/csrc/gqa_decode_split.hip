@@ -21,15 +21,18 @@
 // num_splits == 1 runs the single-pass kernel, so v2 with one split equals v1
 // bit for bit.
 //
-// Two layouts for split mode. With few splits, P = 4 waves share each split
-// (the decomposition above, grid (kv-heads, B, num_splits)). With at least as
-// many splits as one round of one wave per SIMD gives each (request, kv-head)
-// waves, every split is scanned by one wave, and each wave walks a contiguous
-// run of splits with one tile pipeline (gqa_decode_split_range_kernel): the
-// grid stays at the single pass's size whatever the split count, and the
-// splits' states leave as each split ends. A split's state is then the
-// sequential fold of its tiles, which does not depend on which wave scans it
-// or on how many splits that wave takes.
+// Two layouts for split mode. With few splits, P waves share each split (the
+// decomposition above, grid (kv-heads, B, num_splits)): 4, or 8, 12 or 16 on
+// grids that leave CUs idle (waves_per_split in gqa_scan.hpp). With at least
+// as many splits as one round of one wave per SIMD gives each (request,
+// kv-head) waves, every split is scanned by one wave, and each wave walks a
+// contiguous run of splits with one tile pipeline
+// (gqa_decode_split_range_kernel): the grid stays at the single pass's size
+// whatever the split count, and the splits' states are staged in LDS and
+// leave after the wave's last tile. A split's state is then the sequential
+// fold of its tiles, which does not depend on which wave scans it or on how
+// many splits that wave takes. Grids that leave CUs idle with splits of at
+// most 1024 tokens run the matrix-core scan instead (use_mfma_underfilled).
 #include "gqa_device.hpp"
 #include "gqa_launch.hpp"
 #include "gqa_merge.hpp"

@@ -245,3 +245,24 @@ def test_update_traffic_replaces_or_appends(tmp_path):
     pc.update_traffic(str(path), "c2 v2 1 11 21")
     pc.update_traffic(str(path), "c5 v2 balanced 50 60")
     assert path.read_text() == "# header\nc2 v2 1 11 21\nc3 v2 4 30 40\nc5 v2 balanced 50 60\n"
+
+
+@pytest.mark.parametrize("args,want", [
+    (("v2", 4, False, 8, 1, 4, 512, 256), "gqa_decode_mfma_kernel"),   # config 1: short splits, idle CUs
+    (("v1", 4, False, 8, 1, 1, 512, 256), "gqa_decode_mfma_kernel"),
+    (("v2", 4, False, 8, 32, 1, 8192, 256), "gqa_decode_scan_kernel"),  # config 2
+    (("v2", 4, False, 8, 32, 32, 8192, 256), "gqa_decode_split_range_kernel"),
+    (("v2", 4, False, 8, 8, 4, 32768, 256), "gqa_decode_scan_kernel"),  # config 3
+    (("v2", 4, False, 8, 8, 1, 32768, 256), "gqa_decode_scan_kernel"),  # idle CUs, long splits
+    (("v2", 4, False, 8, 8, 16, 32768, 256), "gqa_decode_split_range_kernel"),
+    (("v2", 8, False, 8, 32, 8, 32768, 256), "gqa_decode_mfma_kernel"),
+    (("v2", 8, True, 8, 32, 1, 32768, 256), "gqa_decode_balanced_mfma_kernel"),
+    (("v2", 4, True, 16, 32, 1, 32768, 256), "gqa_decode_balanced_kernel"),
+    (("v0", 4, False, 8, 1, 1, 512, 256), "gqa_decode_v0_kernel")])
+def test_bench_kernel_name(args, want):
+    # bench.py's roofline label follows the launchers' routing (the split-range
+    # layout from 4 * max(1, CUs // (B * Hkv)) splits; the matrix-core scan on
+    # grids of fewer workgroups than CUs with splits of at most 1024 tokens).
+    import bench
+
+    assert bench.kernel_name(*args) == want
