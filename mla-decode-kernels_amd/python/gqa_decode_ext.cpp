@@ -241,7 +241,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"),
         py::arg("seq_lens"), py::arg("scale"), py::arg("num_splits") = 8);
   m.def("gqa_decode_balanced", &gqa_decode_balanced,
-        "token-balanced split-KV decode (paged KV, bf16; GQA groups of at most 4)",
+        "token-balanced split-KV decode (paged KV, bf16; GQA groups of up to 16 q-heads over "
+        "4 or 8 kv-heads, up to 4 over other kv-head counts)",
         py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"),
         py::arg("seq_lens"), py::arg("scale"), py::arg("num_workgroups") = 0);
   m.def("prefer_balanced", &gqa_decode_balanced_preferred,
